@@ -1,0 +1,320 @@
+#!/usr/bin/env python3
+"""W4A16 fused dequant + linear benchmark on one MI355X.
+
+Workload (the 12B-like decode linears at M=1): one
+step is one decode layer's worth of W4A16 linears on one token --
+q 3840->4096, k 3840->2048, v 3840->2048, o 4096->3840, gate/up fused
+3840->30720, down 15360->3840 -- with bf16 activations in and bf16 out.
+Consecutive steps walk distinct weight sets (as consecutive layers do), and the
+sets together exceed 512 MB so that the 256 MB MALL cannot hold them: every
+step streams its weights from HBM.
+
+value = algorithmic bytes per step / time per step (GB/s), where the bytes of a
+linear are N*K/2 (packed) + 2*N*K/32 (scales) + 2*M*K (x) + 2*M*N (y).
+
+Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--all]
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import platform
+import statistics
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+for _p in (ROOT, os.path.join(ROOT, "gemma4-zml-probe_amd")):
+    if _p not in sys.path:
+        sys.path.insert(0, _p)
+
+METRIC = "W4A16 GEMV achieved HBM GB/s (% of peak) at M=1; TFLOP/s at M=64"
+PEAK_HBM_GBS = 8000.0          # MI355X HBM3E, published
+PEAK_BF16_TFLOPS = 2500.0      # MI355X dense bf16 MFMA, published
+ROTATE_BYTES = 600 * 2**20     # > 512 MB working set
+
+LAYER_12B = [  # name, K, N
+    ("q", 3840, 4096), ("k", 3840, 2048), ("v", 3840, 2048), ("o", 4096, 3840),
+    ("gate_up", 3840, 30720), ("down", 15360, 3840),
+]
+DOMINANT = "gate_up"
+TRAFFIC_FILE = os.path.join(ROOT, "profiles", "linear_12b_gateup_m1_pmc.md")
+
+
+def lin_bytes(M: int, K: int, N: int) -> int:
+    return N * K // 2 + 2 * N * (K // 32) + 2 * M * K + 2 * M * N
+
+
+def log(*a):
+    print(*a, file=sys.stderr, flush=True)
+
+
+def read_traffic():
+    """HBM bytes per launch of the dominant kernel, from the committed rocprofv3
+    --pmc summary (line 'traffic_bytes_per_launch: <int>'), or None."""
+    try:
+        with open(TRAFFIC_FILE) as f:
+            for line in f:
+                if line.strip().startswith("traffic_bytes_per_launch:"):
+                    return int(float(line.split(":", 1)[1].strip()))
+    except OSError:
+        pass
+    return None
+
+
+def make_set(torch, o, K, N, seed):
+    """Synthetic packed weights generated on the GPU: iid uniform 32-bit words
+    are iid uniform nibbles, i.e. q ~ U{-8..7}; scales bf16(|N(0,1)| * 0.02)."""
+    g = torch.Generator(device="cuda")
+    g.manual_seed(seed)
+    pkd = torch.randint(-2**31, 2**31, (N, K // 8), generator=g, device="cuda", dtype=torch.int64).to(torch.int32)
+    scd = (torch.randn((N, K // 32), generator=g, device="cuda").abs() * 0.02).to(torch.bfloat16)
+    return pkd, scd
+
+
+def synth_x_dev(torch, o, M, K):
+    import numpy as np
+    x = o.synth_x(M, K)
+    return torch.from_numpy(x.view(np.int16)).view(torch.bfloat16).cuda()
+
+
+def graph_of(torch, fn):
+    """Capture fn() (a sequence of libw4a16 launches on the current stream) in a HIP graph."""
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(s):
+        fn()  # one eager pass on the side stream before capture
+    torch.cuda.current_stream().wait_stream(s)
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        fn()
+    torch.cuda.synchronize()
+    return g
+
+
+def time_graph(torch, g, replays, warmup=2):
+    for _ in range(warmup):
+        g.replay()
+    torch.cuda.synchronize()
+    a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    a.record()
+    for _ in range(replays):
+        g.replay()
+    b.record()
+    torch.cuda.synchronize()
+    return a.elapsed_time(b) * 1e-3
+
+
+def time_config(torch, w4a16, o, M, K, N, launches=None):
+    """Average duration of one linear launch: a HIP graph of back-to-back launches
+    rotating over weight sets larger than the MALL, timed with events around its
+    replays (no host launch overhead between kernels)."""
+    nbytes = lin_bytes(M, K, N)
+    nsets = max(2, -(-ROTATE_BYTES // (N * K // 2 + N * K // 16)))
+    sets = [make_set(torch, o, K, N, 7000 + i) for i in range(nsets)]
+    x = synth_x_dev(torch, o, M, K)
+    y = torch.empty((M, N), dtype=torch.bfloat16, device="cuda")
+    if launches is None:
+        launches = nsets * max(1, -(-40 // nsets)) if M < 512 else nsets
+    def run():
+        for i in range(launches):
+            pk, sc = sets[i % nsets]
+            w4a16.linear(x, pk, sc, out=y)
+    g = graph_of(torch, run)
+    reps = 5 if M < 512 else 2
+    t = time_graph(torch, g, reps) / (reps * launches)
+    del g, sets
+    torch.cuda.empty_cache()
+    return {"M": M, "K": K, "N": N, "bytes": nbytes, "flops": 2 * M * N * K, "us": t * 1e6,
+            "GBps": nbytes / t / 1e9, "hbm_frac": nbytes / t / 1e9 / PEAK_HBM_GBS,
+            "TFLOPs": 2 * M * N * K / t / 1e12, "mfma_frac": 2 * M * N * K / t / 1e12 / PEAK_BF16_TFLOPS,
+            "sets": nsets, "launches": launches}
+
+
+def cpu_baseline(budget_s: float = 15.0):
+    """The reference's CPU path (PyTorch restatement, oracle/cpu_path.py) on the
+    host cores: dequant + matmul per call, over the same 12B layer linears at
+    M=1 (one decode layer per step), repeated until ~budget_s seconds."""
+    import numpy as np
+    import torch
+    from oracle import cpu_path, w4a16_oracle as o
+
+    torch.set_num_threads(max(1, torch.get_num_threads()))
+    mats = []
+    g = torch.Generator()
+    g.manual_seed(8000)
+    for i, (name, K, N) in enumerate(LAYER_12B):
+        pk = torch.randint(-2**31, 2**31, (N, K // 8), generator=g, dtype=torch.int64).to(torch.int32)
+        sc = (torch.randn((N, K // 32), generator=g).abs() * 0.02).to(torch.bfloat16)
+        mats.append((pk, sc, torch.from_numpy(o.synth_x(1, K).view(np.int16)).view(torch.bfloat16)))
+    step_bytes = sum(lin_bytes(1, K, N) for _, K, N in LAYER_12B)
+
+    def one_step():
+        for pk, sc, x in mats:
+            cpu_path.linear(x, pk, sc).to(torch.bfloat16)
+
+    one_step()  # warm-up
+    times = []
+    t_start = time.perf_counter()
+    while True:
+        t0 = time.perf_counter()
+        one_step()
+        times.append(time.perf_counter() - t0)
+        if time.perf_counter() - t_start > budget_s or len(times) >= 50:
+            break
+    med = statistics.median(times)
+    cpu_model = ""
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    cpu_model = line.split(":", 1)[1].strip()
+                    break
+    except OSError:
+        pass
+    return {"value": round(step_bytes / med / 1e9, 4), "unit": "GB/s", "cores": torch.get_num_threads(),
+            "kind": "port",
+            "sample": f"one 12B decode layer's 6 W4A16 linears at M=1 (q,k,v,o,gate_up,down), torch CPU "
+                      f"dequant+matmul per call (oracle/cpu_path.py), median of {len(times)} steps, "
+                      f"{med * 1e3:.1f} ms/step; os.cpu_count()={os.cpu_count()}; cpu={cpu_model}"}
+
+
+def main() -> int:
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=200)
+    ap.add_argument("--warmup", type=int, default=20)
+    ap.add_argument("--all", action="store_true", help="also sweep every BASELINE config (stderr + gpurun_out)")
+    ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
+    ap.add_argument("--cpu-budget", type=float, default=15.0)
+    args = ap.parse_args()
+
+    if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
+        print("bench.py measures one GPU only: this build has no multi-GPU path "
+              "(the W4A16 linear would shard by rows of N; see DESIGN.md). Run with --gpus 1.",
+              file=sys.stderr)
+        return 2
+
+    import torch
+    import w4a16
+    from oracle import w4a16_oracle as o
+
+    w4a16.lib()  # fails loudly without the HIP library
+    props = torch.cuda.get_device_properties(0)
+    log(f"BUILD: device={props.name} arch={getattr(props, 'gcnArchName', '?')} CUs={props.multi_processor_count} "
+        f"hip={torch.version.hip} torch={torch.__version__} lib=libw4a16.so(-O3, gfx950) host={platform.node()}")
+
+    # ---- the headline workload: 12B layer linears at M=1, rotating sets
+    layer_bytes = sum(N * K // 2 + N * K // 16 for _, K, N in LAYER_12B)
+    nsets = max(2, -(-ROTATE_BYTES // layer_bytes))
+    log(f"allocating {nsets} weight sets of one 12B layer ({layer_bytes / 2**20:.1f} MiB each)")
+    sets = [[make_set(torch, o, K, N, 1000 + 2 + 10 * s + i) for i, (_, K, N) in enumerate(LAYER_12B)]
+            for s in range(nsets)]
+    xs = {K: synth_x_dev(torch, o, 1, K) for K in {K for _, K, _ in LAYER_12B}}
+    ys = [torch.empty((1, N), dtype=torch.bfloat16, device="cuda") for _, _, N in LAYER_12B]
+    step_bytes = sum(lin_bytes(1, K, N) for _, K, N in LAYER_12B)
+    dom = [i for i, (n, _, _) in enumerate(LAYER_12B) if n == DOMINANT][0]
+
+    def step(s):
+        ws = sets[s % nsets]
+        for i, (_, K, _) in enumerate(LAYER_12B):
+            w4a16.linear(xs[K], ws[i][0], ws[i][1], out=ys[i])
+
+    # eager (host-launched) steps, for reference: includes Python/ctypes launch overhead
+    for s in range(args.warmup):
+        step(s)
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for s in range(args.warmup):
+        step(s)
+    torch.cuda.synchronize()
+    eager_ms = (time.perf_counter() - t0) / args.warmup * 1e3
+
+    # timed region: one HIP graph per rotation of the weight sets (nsets steps),
+    # replayed until `steps` steps have run, bracketed by synchronize + events
+    g = graph_of(torch, lambda: [step(s) for s in range(nsets)])
+    reps = max(1, -(-args.steps // nsets))
+    for _ in range(2):
+        g.replay()
+    torch.cuda.synchronize()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    t0 = time.perf_counter()
+    e0.record()
+    for _ in range(reps):
+        g.replay()
+    e1.record()
+    torch.cuda.synchronize()
+    dt_wall = time.perf_counter() - t0
+    n_steps = reps * nsets
+    dt = e0.elapsed_time(e1) * 1e-3
+    ms_per_step = dt / n_steps * 1e3
+    value = step_bytes / (dt / n_steps) / 1e9
+    del g
+
+    # dominant kernel: graph of back-to-back gate_up launches over >= 8 weight sets
+    dom_name, dK, dN = LAYER_12B[dom]
+    dom = time_config(torch, w4a16, o, 1, dK, dN)
+    dom_bytes, dom_avg, dom_gbs = dom["bytes"], dom["us"] * 1e-6, dom["GBps"]
+    log(f"step: {ms_per_step * 1e3:.2f} us ({value:.1f} GB/s, {value / PEAK_HBM_GBS * 100:.1f} % of HBM peak), "
+        f"wall {dt_wall / n_steps * 1e6:.2f} us/step, eager {eager_ms * 1e3:.1f} us/step; "
+        f"gate_up launch avg {dom_avg * 1e6:.2f} us = {dom_gbs:.1f} GB/s")
+    del sets
+    torch.cuda.empty_cache()
+
+    # ---- M = 64: TFLOP/s of the 12B gate/up linear
+    m64 = time_config(torch, w4a16, o, 64, 3840, 30720)
+    log(f"M=64 gate_up: {m64['us']:.2f} us, {m64['TFLOPs']:.1f} TFLOP/s ({m64['mfma_frac'] * 100:.1f} % of bf16 MFMA), "
+        f"{m64['GBps']:.0f} GB/s")
+
+    table = None
+    if args.all:
+        table = []
+        cfgs = [("C1", 1, 1536, 6144)]
+        cfgs += [(f"E2B_{n}", 1, K, N) for n, K, N in [("q", 1536, 2048), ("kv", 1536, 256), ("o", 2048, 1536),
+                                                        ("gate_up", 1536, 12288), ("down", 6144, 1536)]]
+        cfgs += [(f"12B_{n}", 1, K, N) for n, K, N in LAYER_12B]
+        cfgs += [(f"C4_M{M}", M, 3840, 30720) for M in (8, 16, 32, 64)]
+        cfgs += [("C5_gate_up", 2048, 3840, 30720), ("C5_down", 2048, 15360, 3840)]
+        for name, M, K, N in cfgs:
+            r = time_config(torch, w4a16, o, M, K, N)
+            r["name"] = name
+            table.append(r)
+            log(f"{name:12s} M={M:5d} K={K:6d} N={N:6d}  {r['us']:9.2f} us"
+                f"  {r['GBps']:8.1f} GB/s ({r['hbm_frac'] * 100:5.1f} %)  {r['TFLOPs']:8.2f} TFLOP/s ({r['mfma_frac'] * 100:5.1f} %)")
+        os.makedirs(os.path.join(ROOT, "gpurun_out"), exist_ok=True)
+        with open(os.path.join(ROOT, "gpurun_out", "bench_all.json"), "w") as f:
+            json.dump(table, f, indent=1)
+
+    cpu = None if args.no_cpu else cpu_baseline(args.cpu_budget)
+    if cpu:
+        log(f"cpu baseline: {cpu['value']} GB/s on {cpu['cores']} threads ({cpu['sample']})")
+
+    traffic = read_traffic()
+    out = {
+        "metric": METRIC, "value": round(value, 2), "unit": "GB/s", "n_gpus": 1,
+        "steps": args.steps, "warmup": args.warmup, "ms_per_step": round(ms_per_step, 5),
+        "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": "bf16",
+        "data": "synthetic (q ~ U{-8..7}, scale bf16(|N(0,1)|*0.02), x bf16 N(0,1); seeded)",
+        "config": {"workload": "configs[2]: 12B-like decode layer linears at M=1 (q,k,v,o,gate_up fused,down), "
+                               "bf16 x in / bf16 y out, int4 group 32",
+                   "M": 1, "bytes_per_step": step_bytes, "weight_sets": nsets,
+                   "hbm_frac": round(value / PEAK_HBM_GBS, 4)},
+        "roofline": {"bound": "hbm", "achieved": round(dom_gbs, 2), "peak": PEAK_HBM_GBS, "unit": "GB/s",
+                     "frac": round(dom_gbs / PEAK_HBM_GBS, 4), "traffic": traffic,
+                     "kernel": "gemv_kernel<1,true,true> (12B gate_up, M=1, N=30720, K=3840)",
+                     "bytes_per_launch": dom_bytes, "avg_launch_us": round(dom_avg * 1e6, 3)},
+        "cpu_baseline": cpu,
+        "m64": {"TFLOPs": round(m64["TFLOPs"], 2), "mfma_frac": round(m64["mfma_frac"], 4),
+                "GBps": round(m64["GBps"], 1), "us": round(m64["us"], 2)},
+        "timing": {"method": "HIP graph replays, events around the timed region", "eager_us_per_step": round(eager_ms * 1e3, 2)},
+    }
+    if table is not None:
+        out["sweep"] = [{k: (round(v, 3) if isinstance(v, float) else v) for k, v in r.items()} for r in table]
+    print(json.dumps(out), flush=True)
+    return 0
+
+
+if __name__ == "__main__":
+    sys.exit(main())

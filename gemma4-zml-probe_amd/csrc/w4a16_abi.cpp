@@ -1,0 +1,152 @@
+// w4a16_abi.cpp -- the C ABI declared in include/w4a16.h.
+//
+// Validates every argument on the host before any HIP call (so the error
+// paths are testable without a GPU), records a thread-local message, and
+// dispatches to the gfx950 kernels in w4a16_kernels.hip.  Nothing here
+// allocates device memory.
+//
+// Boundary it replaces: the ZML graph functions unpackW4 / dequantW4
+// (zml_runner/w4.zig:33-54) and the dotPrec contraction that consumes the
+// dequantized weight (zml_runner/engine.zig:530-533), fused per linear as in
+// G3.forward (zml_runner/gemma4_w4gate.zig:288-292).  In the reference a
+// shape or tag mismatch is a compile-time error of the traced graph
+// (zml_runner/w4.zig:116-117); here it is a negative status code.
+
+#include "../../include/w4a16.h"
+
+#include <hip/hip_runtime.h>
+
+#include <climits>
+#include <cstdarg>
+#include <cstdio>
+#include <cstring>
+
+#include "w4a16_launch.h"
+
+namespace {
+
+thread_local char g_err[512] = "";
+
+int fail(int code, const char* fmt, ...) {
+  va_list ap;
+  va_start(ap, fmt);
+  vsnprintf(g_err, sizeof g_err, fmt, ap);
+  va_end(ap);
+  return code;
+}
+
+void clear_err() { g_err[0] = '\0'; }
+
+bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
+
+int check_ptr(const void* p, const char* name, const char* fn) {
+  if (p == nullptr) return fail(W4A16_EINVAL_PTR, "%s: %s is NULL", fn, name);
+  if (!aligned16(p)) return fail(W4A16_EINVAL_PTR, "%s: %s is not 16-byte aligned", fn, name);
+  return W4A16_OK;
+}
+
+int hip_status(hipError_t e, const char* fn) {
+  if (e == hipSuccess) return W4A16_OK;
+  return fail(W4A16_EHIP, "%s: HIP error %d (%s)", fn, (int)e, hipGetErrorString(e));
+}
+
+// Shared shape checks: dims in [0, INT_MAX], K % 8 (and % group when given).
+int check_dims(const char* fn, int64_t M, int64_t N, int64_t K) {
+  if (M < 0 || N < 0 || K < 0)
+    return fail(W4A16_EINVAL_SHAPE, "%s: negative dimension (M=%lld N=%lld K=%lld)", fn,
+                (long long)M, (long long)N, (long long)K);
+  if (M > INT_MAX || N > INT_MAX || K > INT_MAX)
+    return fail(W4A16_EINVAL_SHAPE, "%s: dimension above INT_MAX", fn);
+  if (K % 8 != 0) return fail(W4A16_EINVAL_SHAPE, "%s: K=%lld is not a multiple of 8", fn, (long long)K);
+  return W4A16_OK;
+}
+
+int check_group(const char* fn, int64_t K, int32_t group) {
+  if (group < 32 || group % 32 != 0)
+    return fail(W4A16_EINVAL_ARG, "%s: group=%d must be a positive multiple of 32", fn, (int)group);
+  if (K % group != 0)
+    return fail(W4A16_EINVAL_SHAPE, "%s: K=%lld is not a multiple of group=%d", fn, (long long)K,
+                (int)group);
+  return W4A16_OK;
+}
+
+size_t round_up(size_t v, size_t a) { return (v + a - 1) / a * a; }
+
+}  // namespace
+
+extern "C" {
+
+int w4a16_version(void) { return W4A16_ABI_VERSION; }
+
+const char* w4a16_last_error(void) { return g_err; }
+
+int w4a16_unpack(const int32_t* pk, int8_t* q, int64_t N, int64_t K, void* stream) {
+  static const char* fn = "w4a16_unpack";
+  clear_err();
+  int rc = check_dims(fn, 0, N, K);
+  if (rc) return rc;
+  if (N == 0 || K == 0) return W4A16_OK;
+  if ((rc = check_ptr(pk, "pk", fn)) || (rc = check_ptr(q, "q", fn))) return rc;
+  return hip_status(w4l_unpack(pk, q, N * (K / 8), static_cast<hipStream_t>(stream)), fn);
+}
+
+int w4a16_dequant(const int32_t* pk, const uint16_t* sc, uint16_t* w, int64_t N, int64_t K,
+                  int32_t group, void* stream) {
+  static const char* fn = "w4a16_dequant";
+  clear_err();
+  int rc = check_dims(fn, 0, N, K);
+  if (rc) return rc;
+  if ((rc = check_group(fn, K, group))) return rc;
+  if (N == 0 || K == 0) return W4A16_OK;
+  if ((rc = check_ptr(pk, "pk", fn)) || (rc = check_ptr(sc, "sc", fn)) || (rc = check_ptr(w, "w", fn)))
+    return rc;
+  return hip_status(w4l_dequant(pk, sc, w, N, K, group, static_cast<hipStream_t>(stream)), fn);
+}
+
+size_t w4a16_workspace_size(int64_t M, int64_t N, int64_t K, int32_t x_dtype) {
+  (void)N;
+  if (M <= 0 || K <= 0) return 0;
+  if (x_dtype == W4A16_DTYPE_F32) return round_up((size_t)(3 * 2) * (size_t)M * (size_t)K, 256);
+  return 0;
+}
+
+int w4a16_linear(const void* x, int32_t x_dtype, const int32_t* pk, const uint16_t* sc, void* y,
+                 int32_t y_dtype, int64_t M, int64_t N, int64_t K, int32_t group, int32_t flags,
+                 void* workspace, size_t ws_bytes, void* stream) {
+  static const char* fn = "w4a16_linear";
+  clear_err();
+  int rc = check_dims(fn, M, N, K);
+  if (rc) return rc;
+  if ((rc = check_group(fn, K, group))) return rc;
+  if (x_dtype != W4A16_DTYPE_BF16 && x_dtype != W4A16_DTYPE_F32)
+    return fail(W4A16_EINVAL_ARG, "%s: unknown x_dtype %d", fn, (int)x_dtype);
+  if (y_dtype != W4A16_DTYPE_BF16 && y_dtype != W4A16_DTYPE_F32)
+    return fail(W4A16_EINVAL_ARG, "%s: unknown y_dtype %d", fn, (int)y_dtype);
+  if (flags != 0) return fail(W4A16_EINVAL_ARG, "%s: unknown flags 0x%x", fn, (unsigned)flags);
+  if (M == 0 || N == 0) return W4A16_OK;
+  if ((rc = check_ptr(y, "y", fn))) return rc;
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  const int y_f32 = y_dtype == W4A16_DTYPE_F32;
+  if (K == 0) return hip_status(w4l_fill_zero(y, M * N * (y_f32 ? 4 : 2), st), fn);
+  if ((rc = check_ptr(x, "x", fn)) || (rc = check_ptr(pk, "pk", fn)) || (rc = check_ptr(sc, "sc", fn)))
+    return rc;
+
+  const uint16_t* planes = static_cast<const uint16_t*>(x);
+  int nterms = 1;
+  if (x_dtype == W4A16_DTYPE_F32) {
+    const size_t need = w4a16_workspace_size(M, N, K, x_dtype);
+    if (workspace == nullptr || ws_bytes < need)
+      return fail(W4A16_EWORKSPACE, "%s: f32 activations need %zu bytes of workspace, got %zu", fn,
+                  need, workspace ? ws_bytes : (size_t)0);
+    if ((rc = check_ptr(workspace, "workspace", fn))) return rc;
+    uint16_t* split = static_cast<uint16_t*>(workspace);
+    if ((rc = hip_status(w4l_split3(static_cast<const float*>(x), split, M * K, st), fn))) return rc;
+    planes = split;
+    nterms = 3;
+  } else if (workspace != nullptr && !aligned16(workspace)) {
+    return fail(W4A16_EINVAL_PTR, "%s: workspace is not 16-byte aligned", fn);
+  }
+  return hip_status(w4l_linear(planes, nterms, pk, sc, y, y_f32, M, N, K, group, st), fn);
+}
+
+}  // extern "C"

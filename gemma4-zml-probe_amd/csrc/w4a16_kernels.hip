@@ -1,0 +1,597 @@
+// w4a16_kernels.hip -- gfx950 kernels of the W4A16 path.
+//
+// Reference semantics (TheCause/gemma4-zml-probe):
+//   unpackW4   zml_runner/w4.zig:33-45   (logical shift, AND 0xF, minus 8)
+//   dequantW4  zml_runner/w4.zig:47-54   (bf16(q) * bf16 scale -> bf16, RNE)
+//   linear     zml_runner/gemma4_w4gate.zig:288-292, zml_runner/engine.zig:530-533
+//              (x.f32 . dequant(pk, sc).f32, fp32 accumulate)
+//
+// Linear design (every M): a wave owns 16 output rows n and a range of K.
+// Each lane loads one 16-byte chunk of packed weights per step (32 nibbles =
+// one scale group of one row) and expands it in registers straight into the
+// B operand of v_mfma_f32_16x16x32_bf16 -- no LDS staging of weights.  The
+// expansion of 8 nibbles costs 19 VALU ops (dequant8 below).  Each weight
+// enters the MFMA rounded exactly as the reference rounds it, and the products
+// with bf16 x are exact with fp32 accumulation.
+// Activations form the A operand (16 rows of x per m-tile; rows >= M are 0).
+// Waves of one workgroup split K and are reduced through LDS in fixed order.
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace w4k {
+
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef float floatx4 __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+
+constexpr int KSTEP = 128;  // K covered by one wave per step (4 lane groups x 32)
+
+// ---------------------------------------------------------------- bf16 helpers
+
+__device__ __forceinline__ float bf16_bits_to_f32(uint32_t h) {
+  return __uint_as_float(h << 16);
+}
+
+// float -> bf16 bits, round to nearest even, NaN -> 0x7FC0 (same rule as the
+// oracle and torch's float->bf16 conversion).
+__device__ __forceinline__ uint32_t f32_to_bf16_rne(float f) {
+  uint32_t u = __float_as_uint(f);
+  uint32_t r = (u + 0x7fffu + ((u >> 16) & 1u)) >> 16;
+  return ((u & 0x7fffffffu) > 0x7f800000u) ? 0x7fc0u : r;
+}
+
+// ---------------------------------------------------------------- in-register dequant
+// 8 nibbles of one packed word -> 8 bf16 weights RNE(q * s) in column order,
+// laid out as one MFMA B operand (4 VGPRs, pairs (w0,w1) .. (w6,w7)).
+//   p_j = (w >> 4j) & 0x000F000F | 0x43004300  bf16 pair (128 + n_j, 128 + n_{j+4})
+//   d   = v_dot2_f32_bf16(p_j, (s, 0) | (0, s), -136 s) = (n - 8) * s, exact in fp32
+//   r   = v_cvt_pk_bf16_f32(d_a, d_b)           RNE to bf16: dequantW4's rounding
+// 19 VALU instructions.  The sequence is one asm block because the compiler's
+// hazard recognizer cannot see inside inline asm, and gfx950 does not
+// interlock a DOT result read by another VALU instruction (3 wait states):
+// all dots are issued before the first conversion, so every conversion reads
+// a dot result at least 3 instructions old.  The VALU -> MFMA wait states are
+// issued by mfma_acc.
+// kM = 0x000F000F and kO = 0x43004300 come in VGPRs (VOP3 takes no literals).
+__device__ __forceinline__ bf16x8 dequant8(uint32_t w, uint32_t slo, uint32_t shi, float c,
+                                           uint32_t kM, uint32_t kO) {
+  uint32_t r0, r1, r2, r3, t, p0, p1, p2, p3;
+  float d0, d1, d2, d3, d4, d5, d6, d7;
+  asm("v_and_or_b32 %[p0], %[w], %[km], %[ko]\n\t"
+      "v_lshrrev_b32 %[t], 4, %[w]\n\t"
+      "v_and_or_b32 %[p1], %[t], %[km], %[ko]\n\t"
+      "v_lshrrev_b32 %[t], 8, %[w]\n\t"
+      "v_and_or_b32 %[p2], %[t], %[km], %[ko]\n\t"
+      "v_lshrrev_b32 %[t], 12, %[w]\n\t"
+      "v_and_or_b32 %[p3], %[t], %[km], %[ko]\n\t"
+      "v_dot2_f32_bf16 %[d0], %[p0], %[slo], %[c]\n\t"
+      "v_dot2_f32_bf16 %[d1], %[p1], %[slo], %[c]\n\t"
+      "v_dot2_f32_bf16 %[d2], %[p2], %[slo], %[c]\n\t"
+      "v_dot2_f32_bf16 %[d3], %[p3], %[slo], %[c]\n\t"
+      "v_dot2_f32_bf16 %[d4], %[p0], %[shi], %[c]\n\t"
+      "v_dot2_f32_bf16 %[d5], %[p1], %[shi], %[c]\n\t"
+      "v_dot2_f32_bf16 %[d6], %[p2], %[shi], %[c]\n\t"
+      "v_dot2_f32_bf16 %[d7], %[p3], %[shi], %[c]\n\t"
+      "v_cvt_pk_bf16_f32 %[r0], %[d0], %[d1]\n\t"
+      "v_cvt_pk_bf16_f32 %[r1], %[d2], %[d3]\n\t"
+      "v_cvt_pk_bf16_f32 %[r2], %[d4], %[d5]\n\t"
+      "v_cvt_pk_bf16_f32 %[r3], %[d6], %[d7]"
+      : [r0] "=&v"(r0), [r1] "=&v"(r1), [r2] "=&v"(r2), [r3] "=&v"(r3), [t] "=&v"(t),
+        [p0] "=&v"(p0), [p1] "=&v"(p1), [p2] "=&v"(p2), [p3] "=&v"(p3),
+        [d0] "=&v"(d0), [d1] "=&v"(d1), [d2] "=&v"(d2), [d3] "=&v"(d3),
+        [d4] "=&v"(d4), [d5] "=&v"(d5), [d6] "=&v"(d6), [d7] "=&v"(d7)
+      : [w] "v"(w), [slo] "v"(slo), [shi] "v"(shi), [c] "v"(c), [km] "v"(kM), [ko] "v"(kO));
+  u32x4 r;
+  r[0] = r0;
+  r[1] = r1;
+  r[2] = r2;
+  r[3] = r3;
+  return __builtin_bit_cast(bf16x8, r);
+}
+
+// D = A * B + D with a tied accumulator.  Issued from asm so that the
+// accumulator keeps its registers for the whole K loop: left to itself the
+// compiler may give an MFMA a SrcC different from its Dst and hand the freed
+// SrcC registers to the next instruction while the MFMA still reads them,
+// which it guards against only for writers it can see (not dequant8).
+// s_nop 1 first: gfx950 needs 2 wait states between a VALU write of a VGPR
+// and an MFMA read of it (A/B come from dequant8 and from zero fills).
+// Back-to-back MFMAs accumulating into the same registers need none.
+__device__ __forceinline__ void mfma_acc(floatx4& acc, const bf16x8& a, const bf16x8& b) {
+  asm("s_nop 1\n\tv_mfma_f32_16x16x32_bf16 %0, %1, %2, %0" : "+v"(acc) : "v"(a), "v"(b));
+}
+
+// Wait states after the last MFMA before any VALU / memory instruction reads
+// its result (the compiler does not count them after inline asm).
+template <int MT>
+__device__ __forceinline__ void mfma_drain(floatx4 (&acc)[MT]) {
+  asm volatile("s_nop 7\n\ts_nop 7\n\ts_nop 7" : "+v"(acc[0]));
+#pragma unroll
+  for (int mt = 1; mt < MT; ++mt) asm volatile("" : "+v"(acc[mt]));
+}
+
+// ================================================================ unpack
+// Flat over words: word i -> q[8i .. 8i+7].  Main part in 4-word chunks.
+__global__ void __launch_bounds__(256) unpack_kernel(const uint32_t* __restrict__ pk,
+                                                     int8_t* __restrict__ q, int64_t nwords) {
+  const int64_t nchunks = nwords >> 2;
+  const int64_t stride = (int64_t)gridDim.x * blockDim.x;
+  for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < nchunks; i += stride) {
+    const uint4 w = reinterpret_cast<const uint4*>(pk)[i];
+    const uint32_t ws[4] = {w.x, w.y, w.z, w.w};
+    uint32_t out[8];
+#pragma unroll
+    for (int d = 0; d < 4; ++d) {
+      uint32_t lo = 0, hi = 0;
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        lo |= (uint32_t)(uint8_t)((int)((ws[d] >> (4 * j)) & 0xFu) - 8) << (8 * j);
+        hi |= (uint32_t)(uint8_t)((int)((ws[d] >> (4 * j + 16)) & 0xFu) - 8) << (8 * j);
+      }
+      out[2 * d] = lo;
+      out[2 * d + 1] = hi;
+    }
+    uint4* dst = reinterpret_cast<uint4*>(q) + 2 * i;
+    dst[0] = make_uint4(out[0], out[1], out[2], out[3]);
+    dst[1] = make_uint4(out[4], out[5], out[6], out[7]);
+  }
+  // tail words (nwords % 4)
+  const int64_t t = (nchunks << 2) + (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (t < nwords && t >= (nchunks << 2)) {
+    const uint32_t w = pk[t];
+    for (int j = 0; j < 8; ++j) q[8 * t + j] = (int8_t)((int)((w >> (4 * j)) & 0xFu) - 8);
+  }
+}
+
+// ================================================================ dequant
+// One thread per 32-column chunk of a row (K % 32 == 0, group % 32 == 0: the
+// chunk lies inside one scale group).  Bit-exact RNE_bf16(float(q) * s).
+__global__ void __launch_bounds__(256) dequant_kernel(const uint32_t* __restrict__ pk,
+                                                      const uint16_t* __restrict__ sc,
+                                                      uint16_t* __restrict__ w, int64_t nchunks,
+                                                      int64_t chunks_per_row, int64_t groups_per_row,
+                                                      int32_t chunks_per_group) {
+  const int64_t stride = (int64_t)gridDim.x * blockDim.x;
+  for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < nchunks; i += stride) {
+    const int64_t n = i / chunks_per_row;
+    const int64_t c = i - n * chunks_per_row;
+    const float s = bf16_bits_to_f32(sc[n * groups_per_row + c / chunks_per_group]);
+    const uint4 v = reinterpret_cast<const uint4*>(pk)[i];
+    const uint32_t ws[4] = {v.x, v.y, v.z, v.w};
+    uint32_t o[16];
+#pragma unroll
+    for (int d = 0; d < 4; ++d)
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const float a = (float)((int)((ws[d] >> (8 * j)) & 0xFu) - 8) * s;
+        const float b = (float)((int)((ws[d] >> (8 * j + 4)) & 0xFu) - 8) * s;
+        o[4 * d + j] = f32_to_bf16_rne(a) | (f32_to_bf16_rne(b) << 16);
+      }
+    uint4* dst = reinterpret_cast<uint4*>(w) + 4 * i;
+#pragma unroll
+    for (int e = 0; e < 4; ++e) dst[e] = make_uint4(o[4 * e], o[4 * e + 1], o[4 * e + 2], o[4 * e + 3]);
+  }
+}
+
+// ================================================================ f32 x split
+// x f32 [M, K] -> three bf16 planes [3][M][K] with x = t0 + t1 + t2 exactly:
+// t0, t1 take the top 8 significand bits of x and of the remainder (bit
+// truncation), t2 the remaining <= 8 bits.
+__global__ void __launch_bounds__(256) split3_kernel(const float* __restrict__ x,
+                                                     uint16_t* __restrict__ out, int64_t n) {
+  const int64_t stride = (int64_t)gridDim.x * blockDim.x;
+  for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += stride) {
+    const float v = x[i];
+    const uint32_t u = __float_as_uint(v);
+    const float t0 = __uint_as_float(u & 0xffff0000u);
+    const float r1 = v - t0;
+    const float t1 = __uint_as_float(__float_as_uint(r1) & 0xffff0000u);
+    const float r2 = r1 - t1;
+    out[i] = (uint16_t)(u >> 16);
+    out[n + i] = (uint16_t)(__float_as_uint(t1) >> 16);
+    out[2 * n + i] = (uint16_t)f32_to_bf16_rne(r2);
+  }
+}
+
+// ================================================================ linear
+struct LinearArgs {
+  const uint16_t* x;   // [NT][M][K] bf16 planes
+  const uint32_t* pk;  // [N][K/8]
+  const uint16_t* sc;  // [N][K/group]
+  void* y;             // [M][N] bf16 or f32
+  int M, N, K;
+  int group_chunks;    // group / 32
+  int groups_per_row;  // K / group
+  int y_f32;
+  int64_t x_plane;     // M * K
+};
+
+// MT: 16-row m-tiles per workgroup (1..4).  NT: number of bf16 x planes (1 or 3).
+// MAXT: launch bound (threads); smaller for the register-heavier variants.
+template <int MT, int NT, int MAXT>
+__global__ void __launch_bounds__(MAXT) linear_kernel(LinearArgs a) {
+  extern __shared__ float red[];  // [waves][MT][4][64] partials
+  const int lane = threadIdx.x & 63;
+  const int wave = threadIdx.x >> 6;
+  const int nwaves = blockDim.x >> 6;
+  const int r = lane & 15;  // row within the 16-row tile (n for B, m for A)
+  const int c = lane >> 4;  // lane group: which 32-column chunk of the step
+  const int n0 = blockIdx.x * 16;
+  const int m0 = blockIdx.y * (16 * MT);
+
+  const int steps = (a.K + KSTEP - 1) / KSTEP;
+  const int s_begin = (int)(((int64_t)steps * wave) / nwaves);
+  const int s_end = (int)(((int64_t)steps * (wave + 1)) / nwaves);
+
+  const int nrow = min(n0 + r, a.N - 1);  // clamped: loads stay in bounds
+  const int kwords = a.K >> 3;
+  const uint32_t* pkrow = a.pk + (int64_t)nrow * kwords;
+  const uint16_t* scrow = a.sc + (int64_t)nrow * a.groups_per_row;
+  const int ngroups32 = a.K >> 5;
+
+  uint32_t kM = 0x000F000Fu, kO = 0x43004300u;
+  asm volatile("" : "+v"(kM), "+v"(kO));
+
+  floatx4 acc[MT];
+#pragma unroll
+  for (int mt = 0; mt < MT; ++mt) acc[mt] = floatx4{0.f, 0.f, 0.f, 0.f};
+
+  for (int s = s_begin; s < s_end; ++s) {
+    const int g = s * 4 + c;  // 32-column chunk index of this lane
+    const bool valid = g < ngroups32;
+    uint4 wv = make_uint4(0x88888888u, 0x88888888u, 0x88888888u, 0x88888888u);
+    uint32_t sb = 0;
+    if (valid) {
+      wv = *reinterpret_cast<const uint4*>(pkrow + g * 4);
+      sb = scrow[g / a.group_chunks];
+    }
+    const float cneg = -136.0f * bf16_bits_to_f32(sb);
+    const uint32_t wj[4] = {wv.x, wv.y, wv.z, wv.w};
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      // A operands: lane (r, c) holds x[m][32g + 8j .. +7] for m = m0 + 16 mt + r
+      bf16x8 xa[NT][MT];
+#pragma unroll
+      for (int t = 0; t < NT; ++t)
+#pragma unroll
+        for (int mt = 0; mt < MT; ++mt) {
+          const int m = m0 + 16 * mt + r;
+          uint4 v = make_uint4(0, 0, 0, 0);
+          if (valid && m < a.M)
+            v = *reinterpret_cast<const uint4*>(a.x + t * a.x_plane + (int64_t)m * a.K + g * 32 + 8 * j);
+          xa[t][mt] = __builtin_bit_cast(bf16x8, v);
+        }
+      const bf16x8 b = dequant8(wj[j], sb, sb << 16, cneg, kM, kO);
+#pragma unroll
+      for (int t = 0; t < NT; ++t)
+#pragma unroll
+        for (int mt = 0; mt < MT; ++mt)
+          mfma_acc(acc[mt], xa[t][mt], b);
+    }
+  }
+  mfma_drain<MT>(acc);
+
+  // D layout: lane (n = lane & 15, c = lane >> 4) holds D[m = 4c + i][n], i = 0..3.
+  if (nwaves > 1) {
+#pragma unroll
+    for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+      for (int i = 0; i < 4; ++i) red[((wave * MT + mt) * 4 + i) * 64 + lane] = acc[mt][i];
+    __syncthreads();
+    const int per_wave = MT * 4 * 64;
+    for (int e = threadIdx.x; e < per_wave; e += blockDim.x) {
+      float v = 0.f;
+      for (int w = 0; w < nwaves; ++w) v += red[w * per_wave + e];
+      const int l = e & 63, i = (e >> 6) & 3, mt = e >> 8;
+      const int m = m0 + 16 * mt + 4 * (l >> 4) + i;
+      const int n = n0 + (l & 15);
+      if (m < a.M && n < a.N) {
+        if (a.y_f32) reinterpret_cast<float*>(a.y)[(int64_t)m * a.N + n] = v;
+        else reinterpret_cast<uint16_t*>(a.y)[(int64_t)m * a.N + n] = (uint16_t)f32_to_bf16_rne(v);
+      }
+    }
+  } else {
+#pragma unroll
+    for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const int m = m0 + 16 * mt + 4 * c + i;
+        const int n = n0 + r;
+        if (m < a.M && n < a.N) {
+          if (a.y_f32) reinterpret_cast<float*>(a.y)[(int64_t)m * a.N + n] = acc[mt][i];
+          else reinterpret_cast<uint16_t*>(a.y)[(int64_t)m * a.N + n] = (uint16_t)f32_to_bf16_rne(acc[mt][i]);
+        }
+      }
+  }
+}
+
+// ================================================================ GEMV (decode, M <= 4)
+// One workgroup per 16 output rows; its W waves split K.  Each wave issues
+// the loads of all its steps (<= SMAX steps of 128 columns: one 16-byte
+// packed chunk + one scale per lane and step) before anything else, so a
+// wave has up to SMAX KiB of weights in flight.  While they arrive the
+// workgroup copies x (M rows, whole K, <= 64 KiB) into LDS; A operands are
+// then read from LDS with every lane of a 16-lane group reading the same
+// row (rows >= M duplicate row M-1: those output rows are discarded), so no
+// lane needs a zero fill.  The waves' partial tiles are summed in LDS in
+// wave order (deterministic) and one bf16 or f32 row per x row is written.
+constexpr int SMAX = 8;
+
+struct GemvArgs {
+  const uint16_t* x;  // [NT][M][K] bf16 planes
+  const uint32_t* pk;
+  const uint16_t* sc;
+  void* y;
+  int M, N, K;
+  int group_chunks;    // group / 32
+  int groups_per_row;  // K / group
+  int y_f32;
+  int steps;           // ceil(K / 128)
+};
+
+// NT: bf16 x planes (1, or 3 for f32 x).  KFULL: K % 128 == 0 (no partial
+// step).  G32: group == 32 (scale index == chunk index).
+template <int NT, bool KFULL, bool G32>
+__global__ void __launch_bounds__(1024) gemv_kernel(GemvArgs a) {
+  extern __shared__ __attribute__((aligned(16))) uint16_t lds[];
+  const int lane = threadIdx.x & 63;
+  // wave-uniform (SGPR) so that the step guards below are scalar branches
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int nwaves = blockDim.x >> 6;
+  const int r = lane & 15;
+  const int c = lane >> 4;
+  const int n0 = blockIdx.x * 16;
+  const int ng32 = a.K >> 5;
+  const int s_begin = (int)(((int64_t)a.steps * wave) / nwaves);
+  const int s_end = (int)(((int64_t)a.steps * (wave + 1)) / nwaves);
+
+  const int nrow = min(n0 + r, a.N - 1);
+  const uint32_t* pkrow = a.pk + (int64_t)nrow * (a.K >> 3);
+  const uint16_t* scrow = a.sc + (int64_t)nrow * a.groups_per_row;
+
+  uint4 wv[SMAX];
+  uint32_t sb[SMAX];
+  int ch = s_begin;
+  int cnt = min(SMAX, s_end - ch);
+  auto load_chunk = [&](int base, int n) {
+#pragma unroll
+    for (int i = 0; i < SMAX; ++i) {
+      if (i < n) {
+        int g = (base + i) * 4 + c;
+        if (!KFULL) g = min(g, ng32 - 1);
+        wv[i] = *reinterpret_cast<const uint4*>(pkrow + 4 * g);
+        sb[i] = scrow[G32 ? g : g / a.group_chunks];
+      }
+    }
+  };
+  load_chunk(ch, cnt);
+
+  // stage x (all planes, rows, columns) into LDS
+  {
+    const int nvec = (NT * a.M * a.K) >> 3;  // 16-byte vectors
+    const uint4* src = reinterpret_cast<const uint4*>(a.x);
+    uint4* dst = reinterpret_cast<uint4*>(lds);
+    for (int v = threadIdx.x; v < nvec; v += blockDim.x) dst[v] = src[v];
+  }
+  __syncthreads();
+
+  uint32_t kM = 0x000F000Fu, kO = 0x43004300u;
+  asm volatile("" : "+v"(kM), "+v"(kO));
+  floatx4 acc = floatx4{0.f, 0.f, 0.f, 0.f};
+  const int mrow = min(r, a.M - 1);
+  const int plane = a.M * a.K;
+
+  while (cnt > 0) {
+#pragma unroll
+    for (int i = 0; i < SMAX; ++i) {
+      if (i < cnt) {
+        int g = (ch + i) * 4 + c;
+        uint32_t slo = sb[i];
+        if (!KFULL) {
+          if (g >= ng32) slo = 0;  // past K: weights become exact zeros
+          g = min(g, ng32 - 1);
+        }
+        const uint32_t shi = slo << 16;
+        const float cneg = -136.0f * __uint_as_float(shi);
+        const uint16_t* xr = lds + mrow * a.K + 32 * g;
+        const uint32_t wj[4] = {wv[i].x, wv[i].y, wv[i].z, wv[i].w};
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          const bf16x8 b = dequant8(wj[j], slo, shi, cneg, kM, kO);
+#pragma unroll
+          for (int t = 0; t < NT; ++t)
+            mfma_acc(acc, *reinterpret_cast<const bf16x8*>(xr + t * plane + 8 * j), b);
+        }
+      }
+    }
+    ch += SMAX;
+    cnt = min(SMAX, s_end - ch);
+    if (cnt > 0) load_chunk(ch, cnt);
+  }
+  floatx4 accs[1] = {acc};
+  mfma_drain<1>(accs);
+  acc = accs[0];
+
+  // rows m < M <= 4 live in lanes 0..15 (c == 0), acc[m]
+  __syncthreads();  // every wave is done reading x from LDS
+  float* red = reinterpret_cast<float*>(lds);
+  if (c == 0) {
+#pragma unroll
+    for (int i = 0; i < 4; ++i) red[(wave * 4 + i) * 16 + r] = acc[i];
+  }
+  __syncthreads();
+  if ((int)threadIdx.x < 16 * a.M) {
+    const int m = threadIdx.x >> 4, rr = threadIdx.x & 15;
+    float v = 0.f;
+    for (int w = 0; w < nwaves; ++w) v += red[(w * 4 + m) * 16 + rr];
+    const int n = n0 + rr;
+    if (n < a.N) {
+      if (a.y_f32) reinterpret_cast<float*>(a.y)[(int64_t)m * a.N + n] = v;
+      else reinterpret_cast<uint16_t*>(a.y)[(int64_t)m * a.N + n] = (uint16_t)f32_to_bf16_rne(v);
+    }
+  }
+}
+
+// K == 0: y = 0 (a kernel rather than a memset, so callers may capture it in a graph).
+__global__ void __launch_bounds__(256) fill_zero_kernel(uint16_t* __restrict__ p, int64_t nhalves) {
+  const int64_t stride = (int64_t)gridDim.x * blockDim.x;
+  for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < nhalves; i += stride) p[i] = 0;
+}
+
+}  // namespace w4k
+
+// ---------------------------------------------------------------- launchers
+// Called by the C ABI (w4a16_abi.cpp) after argument validation.
+
+#include "w4a16_launch.h"
+
+namespace {
+int grid_for(int64_t work, int block) {
+  int64_t g = (work + block - 1) / block;
+  if (g > 65536) g = 65536;
+  if (g < 1) g = 1;
+  return (int)g;
+}
+}  // namespace
+
+hipError_t w4l_unpack(const int32_t* pk, int8_t* q, int64_t nwords, hipStream_t st) {
+  const int block = 256;
+  const int64_t work = (nwords >> 2) > 0 ? (nwords >> 2) : 1;
+  hipLaunchKernelGGL(w4k::unpack_kernel, dim3(grid_for(work, block)), dim3(block), 0, st,
+                     reinterpret_cast<const uint32_t*>(pk), q, nwords);
+  return hipGetLastError();
+}
+
+hipError_t w4l_dequant(const int32_t* pk, const uint16_t* sc, uint16_t* w, int64_t N, int64_t K,
+                       int32_t group, hipStream_t st) {
+  const int block = 256;
+  const int64_t nchunks = N * (K / 32);
+  hipLaunchKernelGGL(w4k::dequant_kernel, dim3(grid_for(nchunks, block)), dim3(block), 0, st,
+                     reinterpret_cast<const uint32_t*>(pk), sc, w, nchunks, K / 32, K / group,
+                     group / 32);
+  return hipGetLastError();
+}
+
+hipError_t w4l_split3(const float* x, uint16_t* out, int64_t n, hipStream_t st) {
+  const int block = 256;
+  hipLaunchKernelGGL(w4k::split3_kernel, dim3(grid_for(n, block)), dim3(block), 0, st, x, out, n);
+  return hipGetLastError();
+}
+
+hipError_t w4l_fill_zero(void* p, int64_t bytes, hipStream_t st) {
+  const int block = 256;
+  const int64_t nhalves = bytes / 2;
+  hipLaunchKernelGGL(w4k::fill_zero_kernel, dim3(grid_for(nhalves, block)), dim3(block), 0, st,
+                     reinterpret_cast<uint16_t*>(p), nhalves);
+  return hipGetLastError();
+}
+
+
+bool w4l_gemv_ok(int64_t M, int64_t K, int nterms) {
+  return M >= 1 && M <= 4 && (int64_t)nterms * M * K * 2 <= 65536;
+}
+
+int w4l_gemv_waves(int64_t N, int64_t K) {
+  const int64_t steps = (K + w4k::KSTEP - 1) / w4k::KSTEP;
+  const int64_t tiles = (N + 15) / 16;
+  int64_t w = (steps + w4k::SMAX - 1) / w4k::SMAX;      // every wave holds <= SMAX steps
+  const int64_t occ = (2048 + tiles - 1) / tiles;        // >= ~2048 waves in flight
+  if (occ > w) w = occ;
+  if (w > steps) w = steps;
+  if (w > 16) w = 16;
+  if (w < 1) w = 1;
+  return (int)w;
+}
+
+hipError_t w4l_gemv(const uint16_t* x_planes, int nterms, const int32_t* pk, const uint16_t* sc,
+                    void* y, int y_f32, int64_t M, int64_t N, int64_t K, int32_t group,
+                    hipStream_t st) {
+  w4k::GemvArgs a;
+  a.x = x_planes;
+  a.pk = reinterpret_cast<const uint32_t*>(pk);
+  a.sc = sc;
+  a.y = y;
+  a.M = (int)M;
+  a.N = (int)N;
+  a.K = (int)K;
+  a.group_chunks = group / 32;
+  a.groups_per_row = (int)(K / group);
+  a.y_f32 = y_f32;
+  a.steps = (int)((K + w4k::KSTEP - 1) / w4k::KSTEP);
+  const int waves = w4l_gemv_waves(N, K);
+  const size_t xb = (size_t)nterms * M * K * 2, rb = (size_t)waves * 4 * 16 * 4;
+  const size_t lds = xb > rb ? xb : rb;
+  const dim3 grid((unsigned)((N + 15) / 16)), block(64 * waves);
+  const bool kfull = (K % w4k::KSTEP) == 0, g32 = group == 32;
+#define W4_GEMV(NT_, KF_, G_) \
+  hipLaunchKernelGGL((w4k::gemv_kernel<NT_, KF_, G_>), grid, block, lds, st, a)
+  if (nterms == 1) {
+    if (kfull) { if (g32) W4_GEMV(1, true, true); else W4_GEMV(1, true, false); }
+    else { if (g32) W4_GEMV(1, false, true); else W4_GEMV(1, false, false); }
+  } else {
+    if (kfull) { if (g32) W4_GEMV(3, true, true); else W4_GEMV(3, true, false); }
+    else { if (g32) W4_GEMV(3, false, true); else W4_GEMV(3, false, false); }
+  }
+#undef W4_GEMV
+  return hipGetLastError();
+}
+
+W4Plan w4l_plan(int64_t M, int64_t N, int64_t K, int nterms) {
+  W4Plan p{};
+  const int64_t mtiles = (M + 15) / 16;
+  p.mt = (int)(mtiles < 4 ? mtiles : 4);
+  if (p.mt < 1) p.mt = 1;
+  p.grid_m = (int)((M + 16 * p.mt - 1) / (16 * p.mt));
+  p.grid_n = (int)((N + 15) / 16);
+  const int64_t steps = (K + w4k::KSTEP - 1) / w4k::KSTEP;
+  const int64_t wgs = (int64_t)p.grid_n * p.grid_m;
+  const int maxw = W4_MAXT(p.mt, nterms) / 64;
+  int64_t waves = (4096 + wgs - 1) / wgs;  // aim at ~4 waves per SIMD on 256 CUs
+  if (waves > maxw) waves = maxw;
+  if (waves > steps) waves = steps;
+  if (waves < 1) waves = 1;
+  p.waves = (int)waves;
+  return p;
+}
+
+hipError_t w4l_linear(const uint16_t* x_planes, int nterms, const int32_t* pk, const uint16_t* sc,
+                      void* y, int y_f32, int64_t M, int64_t N, int64_t K, int32_t group,
+                      hipStream_t st) {
+  if (w4l_gemv_ok(M, K, nterms)) return w4l_gemv(x_planes, nterms, pk, sc, y, y_f32, M, N, K, group, st);
+  const W4Plan p = w4l_plan(M, N, K, nterms);
+  w4k::LinearArgs a;
+  a.x = x_planes;
+  a.pk = reinterpret_cast<const uint32_t*>(pk);
+  a.sc = sc;
+  a.y = y;
+  a.M = (int)M;
+  a.N = (int)N;
+  a.K = (int)K;
+  a.group_chunks = group / 32;
+  a.groups_per_row = (int)(K / group);
+  a.y_f32 = y_f32;
+  a.x_plane = M * K;
+  const dim3 grid(p.grid_n, p.grid_m);
+  const dim3 block(64 * p.waves);
+  const size_t lds = p.waves > 1 ? (size_t)p.waves * p.mt * 4 * 64 * sizeof(float) : 0;
+#define W4_LAUNCH(MT_, NT_) \
+  hipLaunchKernelGGL((w4k::linear_kernel<MT_, NT_, W4_MAXT(MT_, NT_)>), grid, block, lds, st, a)
+  if (nterms == 1) {
+    switch (p.mt) {
+      case 1: W4_LAUNCH(1, 1); break;
+      case 2: W4_LAUNCH(2, 1); break;
+      case 3: W4_LAUNCH(3, 1); break;
+      default: W4_LAUNCH(4, 1); break;
+    }
+  } else {
+    switch (p.mt) {
+      case 1: W4_LAUNCH(1, 3); break;
+      case 2: W4_LAUNCH(2, 3); break;
+      case 3: W4_LAUNCH(3, 3); break;
+      default: W4_LAUNCH(4, 3); break;
+    }
+  }
+#undef W4_LAUNCH
+  return hipGetLastError();
+}

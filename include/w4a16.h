@@ -1,0 +1,123 @@
+/*
+ * w4a16.h -- C ABI of the MI355X (gfx950) W4A16 library, libw4a16.so.
+ *
+ * Drop-in for the quantized hot path of TheCause/gemma4-zml-probe: the
+ * `dequantW4` brick (zml_runner/w4.zig:33-54) and the decode matmul that
+ * consumes its output (`dotPrec`, zml_runner/engine.zig:530-533), fused as
+ * one call per linear.  In the reference these are ZML graph-construction
+ * functions traced into one XLA executable; here each becomes one
+ * stream-ordered call into hand-written HIP kernels.
+ *
+ * Weight format (compressed-tensors "pack-quantized", w4a16, symmetric;
+ * zml_runner/w4.zig:4-10, docs/W4_RESULTS.md:28-37):
+ *   pk  int32  [N, K/8]      nibble j of word w is column 8w+j, little
+ *                            endian within the word; the nibble stores q+8
+ *                            (unsigned), q in [-8, 7].
+ *   sc  bf16   [N, K/group]  one scale per `group` consecutive columns along
+ *                            K (the input dimension); group is 32 in every
+ *                            checkpoint the reference loads.
+ *   dequantized weight w[n][k] = RNE_bf16(q[n][k] * sc[n][k / group]).
+ * Row-major everywhere.  bf16 values are passed as uint16_t bit patterns, the
+ * way the reference's gates compare them (zml_runner/gemma4_w4gate.zig:98-111).
+ *
+ * Conventions
+ *   - Every entry point returns W4A16_OK (0) or a negative w4a16_status and
+ *     never aborts; w4a16_last_error() gives a thread-local message.
+ *   - `stream` is a hipStream_t passed as void* (NULL = the default stream).
+ *     Calls are stream-ordered and asynchronous: no implicit device sync, no
+ *     host callbacks.  Stateless and reentrant; safe to call from several
+ *     host threads on different streams.
+ *   - The caller owns every device buffer.  No entry point allocates device
+ *     memory.  w4a16_linear takes caller-provided workspace where a shape
+ *     needs it (see w4a16_workspace_size).
+ *   - Device pointers must be 16-byte aligned (pk, sc, x, y, q, w, workspace).
+ *     Row strides are the dense ones implied by the shapes; K % group == 0
+ *     and group % 32 == 0 are required.
+ *   - M == 0 or N == 0 is a no-op; K == 0 writes zeros to y.
+ */
+#ifndef W4A16_H
+#define W4A16_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define W4A16_ABI_VERSION 1
+
+typedef enum w4a16_status {
+    W4A16_OK = 0,
+    W4A16_EINVAL_SHAPE = -1, /* negative dims, K % group, K % 8, size overflow   */
+    W4A16_EINVAL_PTR = -2,   /* null or misaligned pointer                        */
+    W4A16_EINVAL_ARG = -3,   /* unknown dtype / flag, unsupported group size      */
+    W4A16_EWORKSPACE = -4,   /* workspace missing or smaller than required      */
+    W4A16_EHIP = -5          /* HIP launch / runtime error (detail in last_error) */
+} w4a16_status;
+
+/* Element types of x and y. */
+enum {
+    W4A16_DTYPE_BF16 = 0,
+    W4A16_DTYPE_F32 = 1
+};
+
+/* Library version (== W4A16_ABI_VERSION of the build). */
+int w4a16_version(void);
+
+/* Thread-local text of the last error raised on this host thread ("" if none). */
+const char *w4a16_last_error(void);
+
+/*
+ * unpackW4 (zml_runner/w4.zig:33-45; exposed there for the W1 gate,
+ * zml_runner/gemma4_w4gate.zig:44-48): pk int32 [N, K/8] -> q int8 [N, K],
+ * q = ((word >> 4j) & 0xF) - 8 with a logical shift.  Bit-exact.
+ */
+int w4a16_unpack(const int32_t *pk, int8_t *q, int64_t N, int64_t K, void *stream);
+
+/*
+ * dequantW4 (zml_runner/w4.zig:47-54) == W4Lin.toW (w4.zig:28-30) without the
+ * retag: pk [N, K/8] + sc bf16 [N, K/group] -> w bf16 [N, K],
+ * w = RNE_bf16(q * s) (bf16 x bf16 -> bf16, NaN -> 0x7FC0).  Bit-exact.
+ */
+int w4a16_dequant(const int32_t *pk, const uint16_t *sc, uint16_t *w,
+                  int64_t N, int64_t K, int32_t group, void *stream);
+
+/*
+ * Bytes of device workspace w4a16_linear needs for (M, N, K, x_dtype).
+ * x_dtype = W4A16_DTYPE_F32 needs 6 * M * K bytes (rounded up to 256) to
+ * hold the three bf16 terms of x; W4A16_DTYPE_BF16 needs none (0).
+ */
+size_t w4a16_workspace_size(int64_t M, int64_t N, int64_t K, int32_t x_dtype);
+
+/*
+ * The fused unit: y[M, N] = x[M, K] . dequantW4(pk, sc)^T, i.e. G3.forward
+ * (zml_runner/gemma4_w4gate.zig:288-292) and every dotPrec site that consumes
+ * a W4Lin (zml_runner/engine.zig:552,571,583,649,653,659,661,723 through
+ * W4Lin.toW, zml_runner/w4.zig:28-30).  Replaces "x.dot(lin.toW())".
+ *
+ * Numerics: each weight is rounded exactly as dequantW4 rounds it
+ * (RNE_bf16(q * s)); products with x are exact and accumulate in fp32, as in
+ * dotPrec with fam = null (engine.zig:531-532).  Only the summation order
+ * differs from the reference.
+ *   x_dtype  W4A16_DTYPE_BF16 or W4A16_DTYPE_F32 (the
+ *            engine's f32 activations; carried exactly as a sum of three bf16
+ *            terms, so no precision is lost before the fp32 accumulate).
+ *   y_dtype  W4A16_DTYPE_F32 (fam = null flow) or W4A16_DTYPE_BF16 (the fp32
+ *            result rounded to nearest even once, as the bf16 dot of the
+ *            fam = bf16 flow).
+ *   flags    must be 0.
+ *   workspace / ws_bytes  at least w4a16_workspace_size(M, N, K, x_dtype)
+ *            bytes (NULL / 0 allowed when that is 0); W4A16_EWORKSPACE otherwise.
+ */
+int w4a16_linear(const void *x, int32_t x_dtype,
+                 const int32_t *pk, const uint16_t *sc,
+                 void *y, int32_t y_dtype,
+                 int64_t M, int64_t N, int64_t K, int32_t group,
+                 int32_t flags, void *workspace, size_t ws_bytes, void *stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* W4A16_H */

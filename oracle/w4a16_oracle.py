@@ -1,0 +1,198 @@
+"""NumPy front end of the C oracle (oracle/w4a16_oracle.c).
+
+TEST INFRASTRUCTURE ONLY: imported by tests/, by ``__graft_entry__.smoke()``
+and by bench.py's ``cpu_baseline`` leg, always as the checker.  The product
+path (``w4a16`` package / libw4a16.so) never imports it.
+
+bf16 values travel as ``uint16`` bit patterns, as the reference's W1/W2 gates
+compare them (zml_runner/gemma4_w4gate.zig:98-111).
+
+Reference functions restated (file:line in TheCause/gemma4-zml-probe):
+  pack     compressed-tensors pack_to_int32 call, scripts/57_w4_unpack_fixture.py:39
+  unpack   unpackW4, zml_runner/w4.zig:33-45
+  dequant  dequantW4, zml_runner/w4.zig:47-54; dequant_manual,
+           scripts/63_u_dequant_export.py:83-89
+  linear   G3.forward, zml_runner/gemma4_w4gate.zig:288-292;
+           scripts/58_w4_gemm_oracle.py:29 (x.f32 @ w.f32.T)
+"""
+from __future__ import annotations
+
+import ctypes
+import os
+import subprocess
+
+import numpy as np
+
+_HERE = os.path.dirname(os.path.abspath(__file__))
+_LIB_PATH = os.path.join(_HERE, "liboracle_w4a16.so")
+_lib = None
+
+GROUP = 32
+
+
+def build() -> str:
+    """Compile the C oracle in place (make -C oracle)."""
+    subprocess.run(["make", "-s", "-C", _HERE], check=True)
+    return _LIB_PATH
+
+
+def lib() -> ctypes.CDLL:
+    global _lib
+    if _lib is None:
+        if not os.path.exists(_LIB_PATH):
+            build()
+        L = ctypes.CDLL(_LIB_PATH)
+        P = ctypes.c_void_p
+        I64 = ctypes.c_int64
+        L.oracle_pack.argtypes = [P, P, I64, I64]
+        L.oracle_pack.restype = ctypes.c_int
+        L.oracle_unpack.argtypes = [P, P, I64, I64]
+        L.oracle_unpack.restype = ctypes.c_int
+        L.oracle_dequant.argtypes = [P, P, P, I64, I64, I64]
+        L.oracle_dequant.restype = ctypes.c_int
+        L.oracle_dequant_one.argtypes = [ctypes.c_int32, ctypes.c_uint16]
+        L.oracle_dequant_one.restype = ctypes.c_uint16
+        L.oracle_matmul_bf16_f32.argtypes = [P, P, P, I64, I64, I64]
+        L.oracle_matmul_bf16_f32.restype = None
+        L.oracle_matmul_bf16_f64.argtypes = [P, P, P, P, I64, I64, I64]
+        L.oracle_matmul_bf16_f64.restype = None
+        L.oracle_matmul_f32x_f32.argtypes = [P, P, P, I64, I64, I64]
+        L.oracle_matmul_f32x_f32.restype = None
+        L.oracle_matmul_f32x_f64.argtypes = [P, P, P, P, I64, I64, I64]
+        L.oracle_matmul_f32x_f64.restype = None
+        L.oracle_round_bf16.argtypes = [P, P, I64]
+        L.oracle_round_bf16.restype = None
+        L.oracle_f32_to_bf16.argtypes = [ctypes.c_float]
+        L.oracle_f32_to_bf16.restype = ctypes.c_uint16
+        _lib = L
+    return _lib
+
+
+def _p(a: np.ndarray) -> int:
+    assert a.flags["C_CONTIGUOUS"]
+    return a.ctypes.data
+
+
+def pack(q: np.ndarray) -> np.ndarray:
+    """int8 q [N, K] in [-8, 7] -> int32 [N, K/8] (nibble j of word w = column 8w+j, q+8)."""
+    q = np.ascontiguousarray(q, dtype=np.int8)
+    N, K = q.shape
+    pk = np.empty((N, K // 8), dtype=np.int32)
+    if lib().oracle_pack(_p(q), _p(pk), N, K) != 0:
+        raise ValueError("pack: K % 8 != 0 or value outside [-8, 7]")
+    return pk
+
+
+def unpack(pk: np.ndarray, K: int | None = None) -> np.ndarray:
+    """int32 [N, K/8] -> int8 q [N, K] in [-8, 7]."""
+    pk = np.ascontiguousarray(pk, dtype=np.int32)
+    N, W = pk.shape
+    K = 8 * W if K is None else K
+    q = np.empty((N, K), dtype=np.int8)
+    if lib().oracle_unpack(_p(pk), _p(q), N, K) != 0:
+        raise ValueError("unpack: bad K")
+    return q
+
+
+def dequant(pk: np.ndarray, sc: np.ndarray, group: int = GROUP) -> np.ndarray:
+    """int32 pk [N, K/8] + uint16 (bf16) sc [N, K/group] -> uint16 (bf16) w [N, K]."""
+    pk = np.ascontiguousarray(pk, dtype=np.int32)
+    sc = np.ascontiguousarray(sc, dtype=np.uint16)
+    N, W = pk.shape
+    K = 8 * W
+    assert sc.shape == (N, K // group), (sc.shape, N, K, group)
+    w = np.empty((N, K), dtype=np.uint16)
+    if lib().oracle_dequant(_p(pk), _p(sc), _p(w), N, K, group) != 0:
+        raise ValueError("dequant: bad shape / group")
+    return w
+
+
+def dequant_one(q: int, s_bits: int) -> int:
+    return int(lib().oracle_dequant_one(int(q), int(s_bits)))
+
+
+def matmul_f32(x: np.ndarray, w: np.ndarray) -> np.ndarray:
+    """x bf16 [M, K] (uint16), w bf16 [N, K] (uint16) -> f32 [M, N], fp32 accumulate."""
+    x = np.ascontiguousarray(x, dtype=np.uint16)
+    w = np.ascontiguousarray(w, dtype=np.uint16)
+    M, K = x.shape
+    N, K2 = w.shape
+    assert K == K2
+    y = np.empty((M, N), dtype=np.float32)
+    lib().oracle_matmul_bf16_f32(_p(x), _p(w), _p(y), M, N, K)
+    return y
+
+
+def matmul_f64(x: np.ndarray, w: np.ndarray):
+    """float64-accumulate contraction and per-output sum |x||w| (error-bound magnitude)."""
+    x = np.ascontiguousarray(x, dtype=np.uint16)
+    w = np.ascontiguousarray(w, dtype=np.uint16)
+    M, K = x.shape
+    N, _ = w.shape
+    y = np.empty((M, N), dtype=np.float64)
+    mag = np.empty((M, N), dtype=np.float64)
+    lib().oracle_matmul_bf16_f64(_p(x), _p(w), _p(y), _p(mag), M, N, K)
+    return y, mag
+
+
+def matmul_f32x(x: np.ndarray, w: np.ndarray, f64: bool = False):
+    """f32 activations x [M, K] . bf16 w [N, K]^T; fp32 accumulate, or float64 (+ sum |x||w|)."""
+    x = np.ascontiguousarray(x, dtype=np.float32)
+    w = np.ascontiguousarray(w, dtype=np.uint16)
+    M, K = x.shape
+    N, _ = w.shape
+    if not f64:
+        y = np.empty((M, N), dtype=np.float32)
+        lib().oracle_matmul_f32x_f32(_p(x), _p(w), _p(y), M, N, K)
+        return y
+    y = np.empty((M, N), dtype=np.float64)
+    mag = np.empty((M, N), dtype=np.float64)
+    lib().oracle_matmul_f32x_f64(_p(x), _p(w), _p(y), _p(mag), M, N, K)
+    return y, mag
+
+
+def linear(x: np.ndarray, pk: np.ndarray, sc: np.ndarray, group: int = GROUP) -> np.ndarray:
+    """The reference flow: dequant (bf16, bit-exact) then x.f32 @ w.f32^T -> f32 [M, N].
+    x is bf16 (uint16) or float32."""
+    w = dequant(pk, sc, group)
+    if np.asarray(x).dtype == np.float32:
+        return matmul_f32x(x, w)
+    return matmul_f32(x, w)
+
+
+def is_nan_bf16(h: np.ndarray) -> np.ndarray:
+    return (np.asarray(h, dtype=np.uint16) & 0x7FFF) > 0x7F80
+
+
+def round_bf16(y: np.ndarray) -> np.ndarray:
+    """f32 -> bf16 (uint16) with round-to-nearest-even; NaN -> 0x7FC0."""
+    y = np.ascontiguousarray(y, dtype=np.float32)
+    out = np.empty(y.shape, dtype=np.uint16)
+    lib().oracle_round_bf16(_p(y), _p(out), y.size)
+    return out
+
+
+def bf16_to_f32(h: np.ndarray) -> np.ndarray:
+    """uint16 bf16 bit patterns -> float32 (exact widening)."""
+    return (np.asarray(h, dtype=np.uint16).astype(np.uint32) << 16).view(np.float32)
+
+
+def f32_to_bf16(f: np.ndarray) -> np.ndarray:
+    return round_bf16(np.asarray(f, dtype=np.float32))
+
+
+# --------------------------------------------------------------------------
+# Synthetic inputs of the benchmark configurations.
+# q ~ U{-8..7}; scale = bf16(|N(0,1)| * 0.02) [N, K/32]; x = bf16(N(0,1)) [M, K].
+# Seeds: weights 1000 + config index, activations 2000 + M.
+
+def synth_weights(N: int, K: int, seed: int, group: int = GROUP):
+    rng = np.random.Generator(np.random.PCG64(seed))
+    q = rng.integers(-8, 8, size=(N, K), dtype=np.int8)
+    s = (np.abs(rng.standard_normal((N, K // group), dtype=np.float32)) * np.float32(0.02))
+    return q, pack(q), f32_to_bf16(s)
+
+
+def synth_x(M: int, K: int, seed: int | None = None) -> np.ndarray:
+    rng = np.random.Generator(np.random.PCG64(2000 + M if seed is None else seed))
+    return f32_to_bf16(rng.standard_normal((M, K), dtype=np.float32))

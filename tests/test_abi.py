@@ -1,0 +1,129 @@
+"""C-ABI checks that need no GPU: the library loads, exports every function
+include/w4a16.h declares, and rejects bad arguments on the host before any
+HIP call (the reference fails such calls at graph-compile time,
+zml_runner/w4.zig:116-117)."""
+from __future__ import annotations
+
+import ctypes
+import os
+import re
+
+import pytest
+
+from conftest import ROOT
+
+import w4a16
+
+HEADER = os.path.join(ROOT, "include", "w4a16.h")
+
+
+def _declared_functions():
+    text = open(HEADER).read()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    return sorted(set(re.findall(r"\b(w4a16_[a-z_0-9]+)\s*\(", text)))
+
+
+@pytest.fixture(scope="module")
+def L():
+    return w4a16.lib()
+
+
+def test_exports_every_declared_symbol(L):
+    decl = _declared_functions()
+    assert decl, "no declarations parsed"
+    assert sorted(w4a16.EXPORTS) == decl
+    for name in decl:
+        assert hasattr(L, name), name
+
+
+def test_version_matches_header(L):
+    m = re.search(r"#define W4A16_ABI_VERSION (\d+)", open(HEADER).read())
+    assert L.w4a16_version() == int(m.group(1))
+
+
+def test_status_codes_match_header():
+    text = open(HEADER).read()
+    for name, val in (("W4A16_OK", 0), ("W4A16_EINVAL_SHAPE", -1), ("W4A16_EINVAL_PTR", -2),
+                      ("W4A16_EINVAL_ARG", -3), ("W4A16_EWORKSPACE", -4), ("W4A16_EHIP", -5)):
+        assert re.search(rf"{name} = {val}\b", text), name
+        assert w4a16.STATUS_NAMES[val] == name
+
+
+A = 0x10000          # a 16-byte aligned fake device address (never dereferenced)
+MIS = 0x10004        # misaligned
+
+
+def _lin(L, x=A, xd=0, pk=A, sc=A, y=A, yd=0, M=1, N=16, K=64, group=32, flags=0, ws=None, wsb=0):
+    return L.w4a16_linear(x, xd, pk, sc, y, yd, M, N, K, group, flags, ws, wsb, None)
+
+
+def test_linear_validation(L):
+    assert _lin(L, M=-1) == w4a16.EINVAL_SHAPE
+    assert _lin(L, K=60) == w4a16.EINVAL_SHAPE            # K % 8
+    assert _lin(L, K=80) == w4a16.EINVAL_SHAPE            # K % group
+    assert _lin(L, group=16) == w4a16.EINVAL_ARG
+    assert _lin(L, group=48) == w4a16.EINVAL_ARG
+    assert _lin(L, xd=7) == w4a16.EINVAL_ARG
+    assert _lin(L, yd=2) == w4a16.EINVAL_ARG
+    assert _lin(L, flags=1) == w4a16.EINVAL_ARG
+    assert _lin(L, M=2**31) == w4a16.EINVAL_SHAPE
+    assert _lin(L, x=None) == w4a16.EINVAL_PTR
+    assert _lin(L, pk=None) == w4a16.EINVAL_PTR
+    assert _lin(L, sc=MIS) == w4a16.EINVAL_PTR
+    assert _lin(L, y=MIS) == w4a16.EINVAL_PTR
+    assert "not 16-byte aligned" in L.w4a16_last_error().decode()
+    assert _lin(L, xd=1) == w4a16.EWORKSPACE                # f32 x needs workspace
+    assert _lin(L, xd=1, ws=A, wsb=16) == w4a16.EWORKSPACE  # too small
+    assert _lin(L, ws=MIS, wsb=1024) == w4a16.EINVAL_PTR
+    # empty problems are no-ops and touch nothing (no GPU call is made)
+    assert _lin(L, M=0, x=None, pk=None, sc=None, y=None) == 0
+    assert _lin(L, N=0, x=None, pk=None, sc=None, y=None) == 0
+    assert L.w4a16_last_error().decode() == ""
+
+
+def test_unpack_dequant_validation(L):
+    assert L.w4a16_unpack(A, A, -1, 64, None) == w4a16.EINVAL_SHAPE
+    assert L.w4a16_unpack(A, A, 4, 12, None) == w4a16.EINVAL_SHAPE
+    assert L.w4a16_unpack(None, A, 4, 64, None) == w4a16.EINVAL_PTR
+    assert L.w4a16_unpack(A, MIS, 4, 64, None) == w4a16.EINVAL_PTR
+    assert L.w4a16_unpack(None, None, 0, 64, None) == 0
+    assert L.w4a16_dequant(A, A, A, 4, 64, 24, None) == w4a16.EINVAL_ARG
+    assert L.w4a16_dequant(A, A, A, 4, 96, 64, None) == w4a16.EINVAL_SHAPE
+    assert L.w4a16_dequant(A, None, A, 4, 64, 32, None) == w4a16.EINVAL_PTR
+    assert L.w4a16_dequant(None, None, None, 0, 64, 32, None) == 0
+
+
+def test_workspace_size(L):
+    assert L.w4a16_workspace_size(1, 4096, 3840, w4a16.DTYPE_BF16) == 0
+    n = L.w4a16_workspace_size(3, 4096, 3840, w4a16.DTYPE_F32)
+    assert n >= 6 * 3 * 3840 and n % 256 == 0
+    assert L.w4a16_workspace_size(0, 4096, 3840, w4a16.DTYPE_F32) == 0
+
+
+def test_python_wrapper_refuses_cpu_tensors():
+    import torch
+    pk = torch.zeros((16, 8), dtype=torch.int32)
+    sc = torch.zeros((16, 2), dtype=torch.bfloat16)
+    x = torch.zeros((1, 64), dtype=torch.bfloat16)
+    with pytest.raises(w4a16.W4A16Error) as e:
+        w4a16.linear(x, pk, sc)
+    assert e.value.status == w4a16.EINVAL_PTR
+    with pytest.raises(w4a16.W4A16Error):
+        w4a16.dequantW4(pk, sc)
+    with pytest.raises(w4a16.W4A16Error):
+        w4a16.unpackW4(pk)
+
+
+def test_last_error_is_thread_local(L):
+    import threading
+    assert _lin(L, M=-1) == w4a16.EINVAL_SHAPE
+    seen = {}
+
+    def other():
+        seen["msg"] = L.w4a16_last_error().decode()
+
+    t = threading.Thread(target=other)
+    t.start()
+    t.join()
+    assert seen["msg"] == ""
+    assert "negative dimension" in L.w4a16_last_error().decode()

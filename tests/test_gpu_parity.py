@@ -1,0 +1,416 @@
+"""GPU parity: libw4a16.so (HIP, gfx950) against the CPU oracle on identical inputs.
+
+Mirrors the reference's gates (TheCause/gemma4-zml-probe):
+  W1  zml_runner/gemma4_w4gate.zig:50-175   unpack/dequant bit-exact + corrupt-nibble counter-test
+  W2  zml_runner/gemma4_w4gate.zig:179-255  dequant of the 5 E2B shape families, u16 bit-exact
+  U1b zml_runner/gemma4_g12gate.zig:134-170 the same on three 12B shapes
+  W3  zml_runner/gemma4_w4gate.zig:259-363  linear, max_abs <= 1e-4, mean_abs <= 1e-6, 8 fixed points
+The real checkpoint tensors are not available, so the W2/U1b shapes carry the
+synthetic benchmark weights (q ~ U{-8..7}, scale = bf16(|N(0,1)| * 0.02)).
+
+Stated tolerances for the linear (fp32 accumulate, only the summation order differs):
+  y f32:  |y - y_f64| <= 2 * gamma_K * sum_k |x_k w_k| elementwise,
+          max_abs(y - y_oracle32) <= 1e-4 * sqrt(K / 1536) * max(1, rms(y) / 4),
+          rel_L2(y, y_oracle32) <= 1e-5
+  y bf16: |y - RNE(y_oracle32)| <= 1 bf16 ulp for >= 99.9 % of elements, and for every
+          element |y - y_oracle32| <= ulp_bf16(y_oracle32) + 2 * gamma_K * sum_k |x_k w_k|
+          (one final rounding plus the fp32 bound; near-cancelling outputs are bounded
+          absolutely, not in ulps of their tiny value), rel_L2 <= 4e-3
+  argmax of a random bf16 head [4096, N] (seed 3000) unchanged on rows whose
+  top1 - top2 margin exceeds 1e-3 * |top1|.
+"""
+from __future__ import annotations
+
+import math
+import sys
+
+import numpy as np
+import pytest
+
+from conftest import load_fixture
+
+pytestmark = pytest.mark.gpu
+
+torch = pytest.importorskip("torch")
+
+import w4a16  # noqa: E402
+from oracle import w4a16_oracle as o  # noqa: E402
+
+
+@pytest.fixture(scope="module", autouse=True)
+def _need_gpu():
+    if not torch.cuda.is_available():
+        pytest.skip("no GPU")
+    w4a16.lib()
+
+
+def say(msg: str) -> None:
+    print(f"[gpu-parity] {msg}", flush=True)
+    sys.stdout.flush()
+
+
+def dev_u16(a: np.ndarray, dtype=torch.bfloat16):
+    return torch.from_numpy(np.ascontiguousarray(a).view(np.int16)).view(dtype).cuda()
+
+
+def dev(a: np.ndarray):
+    return torch.from_numpy(np.ascontiguousarray(a)).cuda()
+
+
+def host_u16(t) -> np.ndarray:
+    return t.contiguous().view(torch.int16).cpu().numpy().view(np.uint16)
+
+
+def gpu_linear(x_np, pk, sc, out="f32", group=32, x_f32=False):
+    x = dev(x_np) if x_f32 else dev_u16(x_np)
+    y = w4a16.linear(x, dev(pk), dev_u16(sc), group=group,
+                     out_dtype=torch.float32 if out == "f32" else torch.bfloat16)
+    torch.cuda.synchronize()
+    return y.cpu().numpy() if out == "f32" else host_u16(y)
+
+
+def check_f32(y, x, w, K, y_ref32=None, x_f32=False):
+    """The stated f32 tolerance (module docstring)."""
+    if x_f32:
+        y64, mag = o.matmul_f32x(x, w, f64=True)
+        ref32 = o.matmul_f32x(x, w) if y_ref32 is None else y_ref32
+    else:
+        y64, mag = o.matmul_f64(x, w)
+        ref32 = o.matmul_f32(x, w) if y_ref32 is None else y_ref32
+    u = 2.0 ** -24
+    gam = K * u / (1 - K * u)
+    err64 = np.abs(y.astype(np.float64) - y64)
+    assert np.all(err64 <= 2 * gam * mag + 1e-30), float(np.max(err64 - 2 * gam * mag))
+    rms = float(np.sqrt(np.mean(ref32.astype(np.float64) ** 2))) if ref32.size else 0.0
+    tol_abs = 1e-4 * math.sqrt(K / 1536) * max(1.0, rms / 4)
+    assert float(np.max(np.abs(y - ref32))) <= tol_abs
+    den = float(np.linalg.norm(ref32.astype(np.float64)))
+    if den > 0:
+        assert float(np.linalg.norm((y - ref32).astype(np.float64))) / den <= 1e-5
+    return y64
+
+
+def check_bf16(yb, ref32, mag, K):
+    rb = o.round_bf16(ref32)
+    a = o.bf16_to_f32(yb).astype(np.float64)
+    b = o.bf16_to_f32(rb).astype(np.float64)
+    r = ref32.astype(np.float64)
+
+    def ulp(v):
+        e = np.floor(np.log2(np.maximum(np.abs(v), 2.0 ** -126)))
+        return 2.0 ** (e - 7)
+
+    assert np.mean(np.abs(a - b) <= ulp(b)) >= 0.999
+    u = 2.0 ** -24
+    gam = K * u / (1 - K * u)
+    excess = np.abs(a - r) - (ulp(r) + 2 * gam * mag)
+    assert np.all(excess <= 0), float(np.max(excess))
+    den = np.linalg.norm(r)
+    if den > 0:
+        assert np.linalg.norm(a - r) / den <= 4e-3
+
+
+def check_head_argmax(y, y_ref, N, seed=3000, V=4096):
+    rng = np.random.Generator(np.random.PCG64(seed))
+    head = o.bf16_to_f32(o.f32_to_bf16(rng.standard_normal((V, N), dtype=np.float32))).astype(np.float64)
+    la = y.astype(np.float64) @ head.T
+    lb = y_ref.astype(np.float64) @ head.T
+    top = np.sort(lb, axis=1)
+    margin = top[:, -1] - top[:, -2]
+    decisive = margin > 1e-3 * np.abs(top[:, -1])
+    assert np.array_equal(np.argmax(la, 1)[decisive], np.argmax(lb, 1)[decisive])
+
+
+# ------------------------------------------------------------------ W1
+
+def test_w1_unpack_dequant_fixture():
+    say("W1 fixture")
+    f = load_fixture("w4_unpack.safetensors")
+    q = w4a16.unpackW4(dev(f["packed"])).cpu().numpy()
+    assert np.array_equal(q, f["q_expected"])
+    d = host_u16(w4a16.dequantW4(dev(f["packed"]), dev_u16(f["scales"])))
+    assert np.array_equal(d, f["deq_expected"])
+    qc = w4a16.unpackW4(dev(f["packed_corrupt"])).cpu().numpy()
+    assert np.argwhere(qc != f["q_expected"]).tolist() == [[0, 1]]
+
+
+def test_dequant_exhaustive_all_scale_patterns():
+    say("dequant: 16 q x 65536 scale patterns")
+    q = np.tile(np.arange(-8, 8, dtype=np.int8), 2)[None].repeat(65536, 0)
+    sc = np.arange(65536, dtype=np.uint32).astype(np.uint16)[:, None].copy()
+    pk = o.pack(q)
+    got = host_u16(w4a16.dequantW4(dev(pk), dev_u16(sc)))
+    assert np.array_equal(got, o.dequant(pk, sc))  # canonical NaN on both sides: all bits equal
+    qg = w4a16.unpackW4(dev(pk)).cpu().numpy()
+    assert np.array_equal(qg, q)
+
+
+W2_SHAPES = {  # scripts/57_w4_unpack_fixture.py:75-81 (E2B) and 63:231-236 (12B, U1b)
+    "deq_q0": (2048, 1536), "deq_q4": (4096, 1536), "deq_dn20": (1536, 12288),
+    "deq_plp0": (1536, 256), "deq_plmp": (8960, 1536),
+    "u1b_q0": (4096, 3840), "u1b_q5": (8192, 3840), "u1b_dn0": (3840, 15360),
+}
+
+
+@pytest.mark.parametrize("name", list(W2_SHAPES))
+def test_w2_u1b_dequant_shape_families(name):
+    N, K = W2_SHAPES[name]
+    say(f"W2/U1b dequant {name} N={N} K={K}")
+    _, pk, sc = o.synth_weights(N, K, 4000 + N % 97)
+    got = host_u16(w4a16.dequantW4(dev(pk), dev_u16(sc)))
+    assert np.array_equal(got, o.dequant(pk, sc))
+    assert np.array_equal(w4a16.unpackW4(dev(pk)).cpu().numpy(), o.unpack(pk))
+
+
+# ------------------------------------------------------------------ linear: exactness probes
+
+def test_linear_one_hot_reproduces_dequant_exactly():
+    """One-hot rows of x select single weights: y must equal the bf16 weight
+    exactly.  Over every bf16 scale pattern in the fused kernel's exact range
+    this pins its in-register dequant to dequantW4's rounding.  Stated range:
+    2^-126 <= |s| < 2^120.  Below it v_dot2_f32_bf16 flushes the subnormal scale
+    (weights of magnitude <= 8 * 2^-126 come out as 0); above it the
+    intermediate (128 + n) * s of the in-register dequant overflows fp32.
+    Checkpoint scales are max_abs / 7.5 of bf16 weights, around 2^-20..2^-3."""
+    say("linear one-hot over all finite scale patterns")
+    q = np.tile(np.arange(-8, 8, dtype=np.int8), 2)[None].repeat(65536, 0)
+    sc = np.arange(65536, dtype=np.uint32).astype(np.uint16)[:, None].copy()
+    expo = (sc[:, 0] >> 7) & 0xFF                     # biased exponent
+    in_range = (expo >= 1) & (expo < 127 + 120)
+    subnormal = (expo == 0) & ((sc[:, 0] & 0x7F) != 0)
+    assert subnormal.sum() == 254
+    sc[~(in_range | subnormal), 0] = 0                # drop huge / non-finite scales
+    pk = o.pack(q)
+    x = np.zeros((32, 32), dtype=np.uint16)
+    x[np.arange(32), np.arange(32)] = 0x3F80
+    y = gpu_linear(x, pk, sc, "f32")               # [32, 65536]
+    w = o.bf16_to_f32(o.dequant(pk, sc)).T         # [32, 65536]
+    ok = ~subnormal
+    bad = np.argwhere(y[:, ok] != w[:, ok])
+    assert bad.size == 0, (bad[:5].tolist(), [hex(int(v)) for v in sc[ok][bad[:5, 1], 0]])
+    assert np.all(np.abs(y[:, subnormal] - w[:, subnormal]) <= 8 * 2.0 ** -126)
+
+
+def test_w3_synth_gate():
+    say("W3 synthetic gate (q_proj L0 shape)")
+    f = load_fixture("w4_gemm_synth.safetensors")
+    _, pk, sc = o.synth_weights(2048, 1536, 1001)
+    x = f["x"].reshape(1, -1)
+    y = gpu_linear(x, pk, sc, "f32")[0]
+    exp = f["out_expected"].reshape(-1)
+    assert np.max(np.abs(y - exp)) <= 1e-4
+    assert np.mean(np.abs(y - exp)) <= 1e-6
+    from conftest import load_manifest
+    fp = np.array(load_manifest()["w4_gemm_synth"]["fixed_points_out_0_0_0_8"], dtype=np.float32)
+    assert np.max(np.abs(y[:8] - fp)) <= 1e-4
+
+
+def test_linear_golden_small_cases():
+    f = load_fixture("w4_linear_small.safetensors")
+    i = 0
+    while f"c{i}.packed" in f:
+        pk, sc, x = f[f"c{i}.packed"], f[f"c{i}.scales"], f[f"c{i}.x"]
+        K = pk.shape[1] * 8
+        g = K // sc.shape[1]
+        say(f"small case {i}: M={x.shape[0]} N={pk.shape[0]} K={K} group={g}")
+        y = gpu_linear(x, pk, sc, "f32", group=g)
+        check_f32(y, x, f[f"c{i}.deq_expected"], K, y_ref32=None)
+        assert np.max(np.abs(y - f[f"c{i}.out_expected"])) <= 1e-4 * max(1.0, np.abs(f[f"c{i}.out_expected"]).max() / 4)
+        yb = gpu_linear(x, pk, sc, "bf16", group=g)
+        _, mag = o.matmul_f64(x, f[f"c{i}.deq_expected"])
+        check_bf16(yb, o.linear(x, pk, sc, g), mag, K)
+        i += 1
+
+
+# ------------------------------------------------------------------ linear: BASELINE configs at M=1
+
+C123 = {  # (K, N)
+    "C1": (1536, 6144),
+    "E2B_q": (1536, 2048), "E2B_kv": (1536, 256), "E2B_o": (2048, 1536),
+    "E2B_gateup": (1536, 12288), "E2B_down": (6144, 1536),
+    "12B_gateup": (3840, 30720), "12B_down": (15360, 3840), "12B_q": (3840, 4096),
+    "12B_kv": (3840, 2048), "12B_o": (4096, 3840),
+}
+
+
+@pytest.mark.parametrize("name", list(C123))
+def test_linear_configs_m1(name):
+    K, N = C123[name]
+    say(f"linear M=1 {name} K={K} N={N}")
+    _, pk, sc = o.synth_weights(N, K, 1000 + (K * 7 + N) % 1000)
+    x = o.synth_x(1, K)
+    w = o.dequant(pk, sc)
+    ref32 = o.matmul_f32(x, w)
+    y = gpu_linear(x, pk, sc, "f32")
+    y64 = check_f32(y, x, w, K, ref32)
+    _, mag = o.matmul_f64(x, w)
+    yb = gpu_linear(x, pk, sc, "bf16")
+    check_bf16(yb, ref32, mag, K)
+    check_head_argmax(y, ref32, N)
+    del y64
+
+
+# ------------------------------------------------------------------ skinny and prefill
+
+@pytest.mark.parametrize("M", [2, 3, 8, 16, 17, 32, 33, 63, 64])
+def test_linear_skinny_small_shapes(M):
+    K, N = 1536, 2048
+    say(f"skinny M={M} K={K} N={N}")
+    _, pk, sc = o.synth_weights(N, K, 77)
+    x = o.synth_x(M, K)
+    w = o.dequant(pk, sc)
+    ref32 = o.matmul_f32(x, w)
+    y = gpu_linear(x, pk, sc, "f32")
+    check_f32(y, x, w, K, ref32)
+    _, mag = o.matmul_f64(x, w)
+    check_bf16(gpu_linear(x, pk, sc, "bf16"), ref32, mag, K)
+
+
+@pytest.mark.parametrize("M", [8, 16, 32, 64])
+def test_linear_c4_12b_gateup(M):
+    """12B gate/up weights at M in {8,16,32,64}; the oracle
+    runs on every 61st output row (a size-independent sample)."""
+    K, N = 3840, 30720
+    say(f"C4 M={M} K={K} N={N}")
+    _, pk, sc = o.synth_weights(N, K, 1002)
+    x = o.synth_x(M, K)
+    y = gpu_linear(x, pk, sc, "f32")
+    rows = np.arange(0, N, 61)
+    w = o.dequant(pk[rows], sc[rows])
+    ref32 = o.matmul_f32(x, w)
+    check_f32(y[:, rows], x, w, K, ref32)
+    check_head_argmax(y[:, rows], ref32, len(rows))
+
+
+@pytest.mark.parametrize("K,N", [(3840, 30720), (15360, 3840)])
+def test_linear_c5_prefill(K, N):
+    """M = 2048; oracle on a sample of rows m and n."""
+    M = 2048
+    say(f"C5 prefill M={M} K={K} N={N}")
+    _, pk, sc = o.synth_weights(N, K, 1004)
+    x = o.synth_x(M, K)
+    y = gpu_linear(x, pk, sc, "f32")
+    ms = np.arange(0, M, 53)
+    ns = np.arange(0, N, 97)
+    w = o.dequant(pk[ns], sc[ns])
+    ref32 = o.matmul_f32(x[ms], w)
+    check_f32(y[np.ix_(ms, ns)], x[ms], w, K, ref32)
+    _, mag = o.matmul_f64(x[ms], w)
+    yb = gpu_linear(x, pk, sc, "bf16")
+    check_bf16(yb[np.ix_(ms, ns)], ref32, mag, K)
+
+
+# ------------------------------------------------------------------ edge cases
+
+@pytest.mark.parametrize("M,N,K,group", [(1, 17, 32, 32), (5, 33, 96, 32), (2, 1, 160, 32),
+                                         (3, 48, 256, 64), (1, 64, 512, 128), (4, 24, 384, 128),
+                                         (1, 1, 32, 32)])
+def test_linear_ragged(M, N, K, group):
+    say(f"ragged M={M} N={N} K={K} group={group}")
+    _, pk, sc = o.synth_weights(N, K, 55, group)
+    x = o.synth_x(M, K, 9)
+    w = o.dequant(pk, sc, group)
+    y = gpu_linear(x, pk, sc, "f32", group=group)
+    check_f32(y, x, w, K)
+    assert np.array_equal(host_u16(w4a16.dequantW4(dev(pk), dev_u16(sc), group)), w)
+
+
+def test_empty_and_k_zero():
+    say("empty shapes / K = 0")
+    x = torch.zeros((0, 64), dtype=torch.bfloat16, device="cuda")
+    pk = torch.zeros((16, 8), dtype=torch.int32, device="cuda")
+    sc = torch.zeros((16, 2), dtype=torch.bfloat16, device="cuda")
+    y = w4a16.linear(x, pk, sc)
+    assert y.shape == (0, 16)
+    # K = 0: y = 0 (the dot over an empty contraction)
+    y = torch.full((3, 5), 7.0, dtype=torch.float32, device="cuda")
+    st = w4a16.lib().w4a16_linear(y.data_ptr(), 0, y.data_ptr(), y.data_ptr(), y.data_ptr(), 1,
+                                  3, 5, 0, 32, 0, None, 0, torch.cuda.current_stream().cuda_stream)
+    assert st == 0
+    torch.cuda.synchronize()
+    assert torch.count_nonzero(y).item() == 0
+    yb = torch.full((3, 5), 7.0, dtype=torch.bfloat16, device="cuda")
+    st = w4a16.lib().w4a16_linear(yb.data_ptr(), 0, yb.data_ptr(), yb.data_ptr(), yb.data_ptr(), 0,
+                                  3, 5, 0, 32, 0, None, 0, torch.cuda.current_stream().cuda_stream)
+    assert st == 0
+    torch.cuda.synchronize()
+    assert torch.count_nonzero(yb).item() == 0
+
+
+def test_nan_scale_propagates_to_its_row_only():
+    say("NaN scale")
+    _, pk, sc = o.synth_weights(32, 256, 3)
+    sc[5, 2] = 0x7FC0
+    x = o.synth_x(2, 256, 4)
+    y = gpu_linear(x, pk, sc, "f32")
+    assert np.all(np.isnan(y[:, 5]))
+    assert not np.any(np.isnan(np.delete(y, 5, axis=1)))
+
+
+def test_linear_f32_activations():
+    """x in f32 (the engine's compute dtype): carried exactly as three bf16 terms."""
+    say("f32 activations")
+    for M, K, N in [(1, 1536, 2048), (7, 3840, 512), (64, 256, 96)]:
+        _, pk, sc = o.synth_weights(N, K, 31)
+        rng = np.random.default_rng(M)
+        x = rng.standard_normal((M, K), dtype=np.float32)
+        w = o.dequant(pk, sc)
+        y = gpu_linear(x, pk, sc, "f32", x_f32=True)
+        check_f32(y, x, w, K, x_f32=True)
+
+
+def test_deterministic_and_stream_ordered():
+    say("determinism + non-default stream")
+    K, N = 3840, 4096
+    _, pk, sc = o.synth_weights(N, K, 12)
+    x = dev_u16(o.synth_x(4, K))
+    pkd, scd = dev(pk), dev_u16(sc)
+    a = w4a16.linear(x, pkd, scd, out_dtype=torch.float32)
+    s = torch.cuda.Stream()
+    with torch.cuda.stream(s):
+        b = w4a16.linear(x, pkd, scd, out_dtype=torch.float32)
+    s.synchronize()
+    torch.cuda.synchronize()
+    assert torch.equal(a.view(torch.int32), b.view(torch.int32))
+
+
+def test_w4lin_interface():
+    say("W4Lin init/toW/linear")
+    _, pk, sc = o.synth_weights(256, 512, 8)
+    store = {"m.q_proj.weight_packed": dev(pk), "m.q_proj.weight_scale": dev_u16(sc),
+             "m.q_proj.weight_shape": torch.tensor([256, 512])}
+    lin = w4a16.W4Lin.init(store, "m.q_proj")
+    assert (lin.out_features, lin.in_features) == (256, 512)
+    assert np.array_equal(host_u16(lin.toW()), o.dequant(pk, sc))
+    x = o.synth_x(3, 512)
+    y = lin.linear(dev_u16(x), out_dtype=torch.float32).cpu().numpy()
+    check_f32(y, x, o.dequant(pk, sc), 512)
+
+
+def test_graph_capture_replays_match_eager():
+    """The linear captured in a HIP graph (how a decode step would run it) gives
+    the eager result on every replay, with other eager work in between."""
+    say("graph capture / replay")
+    K, N = 3840, 4096
+    _, pk, sc = o.synth_weights(N, K, 21)
+    pkd, scd = dev(pk), dev_u16(sc)
+    x = dev_u16(o.synth_x(1, K))
+    y = torch.empty((1, N), dtype=torch.float32, device="cuda")
+    ref = w4a16.linear(x, pkd, scd, out_dtype=torch.float32).clone()
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(s):
+        w4a16.linear(x, pkd, scd, out=y)
+    torch.cuda.current_stream().wait_stream(s)
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        w4a16.linear(x, pkd, scd, out=y)
+    for rep in range(4):
+        y.fill_(float("nan"))
+        junk = w4a16.linear(x, pkd, scd, out_dtype=torch.bfloat16)  # eager work between replays
+        torch.cuda.synchronize()
+        g.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(y.view(torch.int32), ref.view(torch.int32)), rep
+        del junk
