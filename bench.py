@@ -39,7 +39,8 @@ LAYER_12B = [  # name, K, N
     ("gate_up", 3840, 30720), ("down", 15360, 3840),
 ]
 DOMINANT = "gate_up"
-TRAFFIC_FILE = os.path.join(ROOT, "profiles", "linear_12b_gateup_m1_pmc.md")
+DOMINANT_KERNEL = "w4k::gemv_fast_kernel<1, 5, 4, 1, true>"  # the launch the M=1 plan picks for K=3840
+TRAFFIC_FILE = os.path.join(ROOT, "profiles", "gemv_fast_12b_gateup_m1_pmc.md")
 
 
 def lin_bytes(M: int, K: int, N: int) -> int:
@@ -189,6 +190,12 @@ def main() -> int:
     ap.add_argument("--all", action="store_true", help="also sweep every BASELINE config (stderr + gpurun_out)")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--cpu-budget", type=float, default=15.0)
+    ap.add_argument("--only-dominant", action="store_true",
+                    help="run only the dominant kernel's timing (gate_up, M=1): the workload of the committed "
+                         "rocprofv3 kernel-trace and --pmc summaries")
+    ap.add_argument("--copy-calibration", action="store_true",
+                    help="run only a plain device copy of known size (256 MiB read + 256 MiB write, 20 times): "
+                         "the scale for rocprofv3 FETCH_SIZE / WRITE_SIZE")
     args = ap.parse_args()
 
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
@@ -205,6 +212,24 @@ def main() -> int:
     props = torch.cuda.get_device_properties(0)
     log(f"BUILD: device={props.name} arch={getattr(props, 'gcnArchName', '?')} CUs={props.multi_processor_count} "
         f"hip={torch.version.hip} torch={torch.__version__} lib=libw4a16.so(-O3, gfx950) host={platform.node()}")
+
+    if args.copy_calibration:
+        n = 64 * 2**20
+        src = torch.empty(n, dtype=torch.float32, device="cuda").uniform_()
+        dst = torch.empty_like(src)
+        for _ in range(20):
+            dst.copy_(src)
+        torch.cuda.synchronize()
+        print(json.dumps({"copy_calibration": {"read_bytes": 4 * n, "write_bytes": 4 * n, "launches": 20}}), flush=True)
+        return 0
+
+    if args.only_dominant:
+        dom_name, dK, dN = [c for c in LAYER_12B if c[0] == DOMINANT][0]
+        r = time_config(torch, w4a16, o, 1, dK, dN)
+        print(json.dumps({"kernel": DOMINANT_KERNEL, "M": 1, "K": dK, "N": dN, "bytes_per_launch": r["bytes"],
+                          "avg_launch_us": round(r["us"], 3), "GBps": round(r["GBps"], 1),
+                          "launches_run": r["launches"] * 8}), flush=True)
+        return 0
 
     # ---- the headline workload: 12B layer linears at M=1, rotating sets
     layer_bytes = sum(N * K // 2 + N * K // 16 for _, K, N in LAYER_12B)
@@ -303,7 +328,7 @@ def main() -> int:
                    "hbm_frac": round(value / PEAK_HBM_GBS, 4)},
         "roofline": {"bound": "hbm", "achieved": round(dom_gbs, 2), "peak": PEAK_HBM_GBS, "unit": "GB/s",
                      "frac": round(dom_gbs / PEAK_HBM_GBS, 4), "traffic": traffic,
-                     "kernel": "gemv_kernel<1,true,true> (12B gate_up, M=1, N=30720, K=3840)",
+                     "kernel": DOMINANT_KERNEL + " (12B gate_up, M=1, N=30720, K=3840)",
                      "bytes_per_launch": dom_bytes, "avg_launch_us": round(dom_avg * 1e6, 3)},
         "cpu_baseline": cpu,
         "m64": {"TFLOPs": round(m64["TFLOPs"], 2), "mfma_frac": round(m64["mfma_frac"], 4),

@@ -18,6 +18,7 @@
 
 #include <hip/hip_runtime.h>
 #include <stdint.h>
+#include <stdlib.h>
 
 namespace w4k {
 
@@ -58,13 +59,15 @@ __device__ __forceinline__ bf16x8 dequant8(uint32_t w, uint32_t slo, uint32_t sh
                                            uint32_t kM, uint32_t kO) {
   uint32_t r0, r1, r2, r3, t, p0, p1, p2, p3;
   float d0, d1, d2, d3, d4, d5, d6, d7;
-  asm("v_and_or_b32 %[p0], %[w], %[km], %[ko]\n\t"
+  // v_bitop3_b32 with truth table 0xEA computes (a & b) | c; on gfx950 it
+  // issues at twice the rate of v_and_or_b32.
+  asm("v_bitop3_b32 %[p0], %[w], %[km], %[ko] bitop3:0xea\n\t"
       "v_lshrrev_b32 %[t], 4, %[w]\n\t"
-      "v_and_or_b32 %[p1], %[t], %[km], %[ko]\n\t"
+      "v_bitop3_b32 %[p1], %[t], %[km], %[ko] bitop3:0xea\n\t"
       "v_lshrrev_b32 %[t], 8, %[w]\n\t"
-      "v_and_or_b32 %[p2], %[t], %[km], %[ko]\n\t"
+      "v_bitop3_b32 %[p2], %[t], %[km], %[ko] bitop3:0xea\n\t"
       "v_lshrrev_b32 %[t], 12, %[w]\n\t"
-      "v_and_or_b32 %[p3], %[t], %[km], %[ko]\n\t"
+      "v_bitop3_b32 %[p3], %[t], %[km], %[ko] bitop3:0xea\n\t"
       "v_dot2_f32_bf16 %[d0], %[p0], %[slo], %[c]\n\t"
       "v_dot2_f32_bf16 %[d1], %[p1], %[slo], %[c]\n\t"
       "v_dot2_f32_bf16 %[d2], %[p2], %[slo], %[c]\n\t"
@@ -103,7 +106,11 @@ __device__ __forceinline__ void mfma_acc(floatx4& acc, const bf16x8& a, const bf
 }
 
 // Wait states after the last MFMA before any VALU / memory instruction reads
-// its result (the compiler does not count them after inline asm).
+// its result (the compiler does not count them after inline asm).  Needed at
+// every point where compiler-generated code may touch the accumulator: after
+// the K loop, and at the end of every loop body or chunk, since at control-flow
+// joins the compiler may copy the accumulator to other registers with VALU
+// moves that would otherwise read it before the last MFMA has written it.
 template <int MT>
 __device__ __forceinline__ void mfma_drain(floatx4 (&acc)[MT]) {
   asm volatile("s_nop 7\n\ts_nop 7\n\ts_nop 7" : "+v"(acc[0]));
@@ -269,8 +276,8 @@ __global__ void __launch_bounds__(MAXT) linear_kernel(LinearArgs a) {
         for (int mt = 0; mt < MT; ++mt)
           mfma_acc(acc[mt], xa[t][mt], b);
     }
+    mfma_drain<MT>(acc);
   }
-  mfma_drain<MT>(acc);
 
   // D layout: lane (n = lane & 15, c = lane >> 4) holds D[m = 4c + i][n], i = 0..3.
   if (nwaves > 1) {
@@ -307,16 +314,19 @@ __global__ void __launch_bounds__(MAXT) linear_kernel(LinearArgs a) {
 }
 
 // ================================================================ GEMV (decode, M <= 4)
-// One workgroup per 16 output rows; its W waves split K.  Each wave issues
-// the loads of all its steps (<= SMAX steps of 128 columns: one 16-byte
-// packed chunk + one scale per lane and step) before anything else, so a
-// wave has up to SMAX KiB of weights in flight.  While they arrive the
-// workgroup copies x (M rows, whole K, <= 64 KiB) into LDS; A operands are
-// then read from LDS with every lane of a 16-lane group reading the same
-// row (rows >= M duplicate row M-1: those output rows are discarded), so no
-// lane needs a zero fill.  The waves' partial tiles are summed in LDS in
-// wave order (deterministic) and one bf16 or f32 row per x row is written.
-constexpr int SMAX = 8;
+// One workgroup per 16 output rows; its W waves split K.  A "step" covers
+// 256 columns: lane (r = row, c = lane group) loads VPL = 2 consecutive
+// 16-byte packed vectors of its row (64 nibbles = 2 scale groups) and the two
+// bf16 scales as one 32-bit word, so each row is read 128 contiguous bytes at
+// a time.  A wave issues the loads of all its steps (<= SPW) before anything
+// else; while they arrive the workgroup copies x (M rows, whole K, <= 64 KiB
+// minus the reduction area) into LDS.  A operands are then read from LDS with
+// every lane of a 16-lane group reading the same row (rows >= M duplicate row
+// M-1 and are discarded), so no lane needs a zero fill.  The waves' partial
+// tiles are summed in LDS in wave order (deterministic).
+constexpr int VPL = 2;                  // 16-byte vectors per lane per step
+constexpr int GSTEP = 128 * VPL;        // columns per step
+constexpr int SPW = 4;                  // steps a wave keeps in flight
 
 struct GemvArgs {
   const uint16_t* x;  // [NT][M][K] bf16 planes
@@ -327,11 +337,11 @@ struct GemvArgs {
   int group_chunks;    // group / 32
   int groups_per_row;  // K / group
   int y_f32;
-  int steps;           // ceil(K / 128)
+  int steps;           // ceil(K / GSTEP)
 };
 
-// NT: bf16 x planes (1, or 3 for f32 x).  KFULL: K % 128 == 0 (no partial
-// step).  G32: group == 32 (scale index == chunk index).
+// NT: bf16 x planes (1, or 3 for f32 x).  KFULL: K % GSTEP == 0 (no partial
+// step).  G32: group == 32 (scale index == 32-column chunk index).
 template <int NT, bool KFULL, bool G32>
 __global__ void __launch_bounds__(1024) gemv_kernel(GemvArgs a) {
   extern __shared__ __attribute__((aligned(16))) uint16_t lds[];
@@ -343,29 +353,42 @@ __global__ void __launch_bounds__(1024) gemv_kernel(GemvArgs a) {
   const int c = lane >> 4;
   const int n0 = blockIdx.x * 16;
   const int ng32 = a.K >> 5;
-  const int s_begin = (int)(((int64_t)a.steps * wave) / nwaves);
-  const int s_end = (int)(((int64_t)a.steps * (wave + 1)) / nwaves);
+  const int s_begin = (a.steps * wave) / nwaves;
+  const int s_end = (a.steps * (wave + 1)) / nwaves;
 
   const int nrow = min(n0 + r, a.N - 1);
   const uint32_t* pkrow = a.pk + (int64_t)nrow * (a.K >> 3);
   const uint16_t* scrow = a.sc + (int64_t)nrow * a.groups_per_row;
 
-  uint4 wv[SMAX];
-  uint32_t sb[SMAX];
+  uint4 wv[SPW][VPL];
+  uint32_t sv[SPW];  // two bf16 scales (low half: first vector's group)
   int ch = s_begin;
-  int cnt = min(SMAX, s_end - ch);
-  auto load_chunk = [&](int base, int n) {
+  int cnt = min(SPW, s_end - ch);
+  // chunk index (32 columns) of vector v of step s for this lane
+  auto chunk = [&](int s, int v) { return (s * 4 + c) * VPL + v; };
+  auto load_steps = [&](int base, int n) {
 #pragma unroll
-    for (int i = 0; i < SMAX; ++i) {
+    for (int i = 0; i < SPW; ++i) {
       if (i < n) {
-        int g = (base + i) * 4 + c;
-        if (!KFULL) g = min(g, ng32 - 1);
-        wv[i] = *reinterpret_cast<const uint4*>(pkrow + 4 * g);
-        sb[i] = scrow[G32 ? g : g / a.group_chunks];
+#pragma unroll
+        for (int v = 0; v < VPL; ++v) {
+          int g = chunk(base + i, v);
+          if (!KFULL) g = min(g, ng32 - 1);
+          wv[i][v] = *reinterpret_cast<const uint4*>(pkrow + 4 * g);
+        }
+        if (G32 && KFULL) {
+          sv[i] = *reinterpret_cast<const uint32_t*>(scrow + chunk(base + i, 0));
+        } else {
+          int g0 = chunk(base + i, 0), g1 = chunk(base + i, 1);
+          if (!KFULL) { g0 = min(g0, ng32 - 1); g1 = min(g1, ng32 - 1); }
+          const uint32_t s0 = scrow[G32 ? g0 : g0 / a.group_chunks];
+          const uint32_t s1 = scrow[G32 ? g1 : g1 / a.group_chunks];
+          sv[i] = s0 | (s1 << 16);
+        }
       }
     }
   };
-  load_chunk(ch, cnt);
+  load_steps(ch, cnt);
 
   // stage x (all planes, rows, columns) into LDS
   {
@@ -378,47 +401,299 @@ __global__ void __launch_bounds__(1024) gemv_kernel(GemvArgs a) {
 
   uint32_t kM = 0x000F000Fu, kO = 0x43004300u;
   asm volatile("" : "+v"(kM), "+v"(kO));
-  floatx4 acc = floatx4{0.f, 0.f, 0.f, 0.f};
+  floatx4 acc[1] = {floatx4{0.f, 0.f, 0.f, 0.f}};
   const int mrow = min(r, a.M - 1);
   const int plane = a.M * a.K;
+  const uint16_t* xrow = lds + mrow * a.K;
 
   while (cnt > 0) {
 #pragma unroll
-    for (int i = 0; i < SMAX; ++i) {
+    for (int i = 0; i < SPW; ++i) {
       if (i < cnt) {
-        int g = (ch + i) * 4 + c;
-        uint32_t slo = sb[i];
-        if (!KFULL) {
-          if (g >= ng32) slo = 0;  // past K: weights become exact zeros
-          g = min(g, ng32 - 1);
-        }
-        const uint32_t shi = slo << 16;
-        const float cneg = -136.0f * __uint_as_float(shi);
-        const uint16_t* xr = lds + mrow * a.K + 32 * g;
-        const uint32_t wj[4] = {wv[i].x, wv[i].y, wv[i].z, wv[i].w};
 #pragma unroll
-        for (int j = 0; j < 4; ++j) {
-          const bf16x8 b = dequant8(wj[j], slo, shi, cneg, kM, kO);
+        for (int v = 0; v < VPL; ++v) {
+          int g = chunk(ch + i, v);
+          uint32_t slo = v == 0 ? (sv[i] & 0xffffu) : (sv[i] >> 16);
+          if (!KFULL) {
+            if (g >= ng32) slo = 0;  // past K: weights become exact zeros
+            g = min(g, ng32 - 1);
+          }
+          const uint32_t shi = slo << 16;
+          const float cneg = -136.0f * __uint_as_float(shi);
+          const uint16_t* xr = xrow + 32 * g;
+          const uint32_t wj[4] = {wv[i][v].x, wv[i][v].y, wv[i][v].z, wv[i][v].w};
 #pragma unroll
-          for (int t = 0; t < NT; ++t)
-            mfma_acc(acc, *reinterpret_cast<const bf16x8*>(xr + t * plane + 8 * j), b);
+          for (int j = 0; j < 4; ++j) {
+            const bf16x8 bb = dequant8(wj[j], slo, shi, cneg, kM, kO);
+#pragma unroll
+            for (int t = 0; t < NT; ++t)
+              mfma_acc(acc[0], *reinterpret_cast<const bf16x8*>(xr + t * plane + 8 * j), bb);
+          }
         }
       }
     }
-    ch += SMAX;
-    cnt = min(SMAX, s_end - ch);
-    if (cnt > 0) load_chunk(ch, cnt);
+    mfma_drain<1>(acc);
+    ch += SPW;
+    cnt = min(SPW, s_end - ch);
+    if (cnt > 0) load_steps(ch, cnt);
   }
-  floatx4 accs[1] = {acc};
-  mfma_drain<1>(accs);
-  acc = accs[0];
 
   // rows m < M <= 4 live in lanes 0..15 (c == 0), acc[m]
-  __syncthreads();  // every wave is done reading x from LDS
-  float* red = reinterpret_cast<float*>(lds);
+  float* red = reinterpret_cast<float*>(lds + NT * plane);
   if (c == 0) {
 #pragma unroll
-    for (int i = 0; i < 4; ++i) red[(wave * 4 + i) * 16 + r] = acc[i];
+    for (int i = 0; i < 4; ++i) red[(wave * 4 + i) * 16 + r] = acc[0][i];
+  }
+  __syncthreads();
+  if ((int)threadIdx.x < 16 * a.M) {
+    const int m = threadIdx.x >> 4, rr = threadIdx.x & 15;
+    float v = 0.f;
+    for (int w = 0; w < nwaves; ++w) v += red[(w * 4 + m) * 16 + rr];
+    const int n = n0 + rr;
+    if (n < a.N) {
+      if (a.y_f32) reinterpret_cast<float*>(a.y)[(int64_t)m * a.N + n] = v;
+      else reinterpret_cast<uint16_t*>(a.y)[(int64_t)m * a.N + n] = (uint16_t)f32_to_bf16_rne(v);
+    }
+  }
+}
+
+// ---------------------------------------------------------------- GEMV, straight-line variant
+// Same tiling as gemv_kernel, for shapes where K is a multiple of GSTEP and
+// every wave gets exactly NST steps (compile time).  A workgroup covers TPW
+// tiles of 16 rows (TPW * 16 consecutive rows), so that a whole grid fits in
+// one round of resident waves.  All loads are issued unconditionally in a
+// fixed order -- this thread's share of x first (XPT vectors, indices clamped
+// so duplicates rewrite the same LDS slot), then the NST steps of weights and
+// scales of every tile -- so the compiler's wait-count analysis is exact: x is
+// written to LDS as soon as it lands while the weights are still in flight,
+// and each step waits only for its own loads.  (vmcnt is an in-order per-wave
+// counter: a conditional load makes every later wait fall back to "all loads
+// done".)  Tiles past N (odd tile counts) recompute the last tile and are not
+// written.
+template <int NT, int NST, int XPT, int TPW, bool G32>
+__global__ void __launch_bounds__(1024) gemv_fast_kernel(GemvArgs a) {
+  extern __shared__ __attribute__((aligned(16))) uint16_t lds[];
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int nwaves = blockDim.x >> 6;
+  const int r = lane & 15;
+  const int c = lane >> 4;
+  const int s0 = wave * NST;
+  const int ntiles = (a.N + 15) >> 4;
+
+  // 1. x loads (this thread's share), unconditional
+  const int nvec = (NT * a.M * a.K) >> 3;
+  const uint4* xsrc = reinterpret_cast<const uint4*>(a.x);
+  uint4 xv[XPT];
+  int xi[XPT];
+#pragma unroll
+  for (int i = 0; i < XPT; ++i) {
+    xi[i] = min((int)threadIdx.x + i * (int)blockDim.x, nvec - 1);
+    xv[i] = xsrc[xi[i]];
+  }
+
+  // 2. weight and scale loads of this wave's NST steps of every tile, unconditional
+  uint4 wv[TPW][NST][VPL];
+  uint32_t sv[TPW][NST];
+#pragma unroll
+  for (int tp = 0; tp < TPW; ++tp) {
+    const int tile = min((int)blockIdx.x * TPW + tp, ntiles - 1);
+    const int nrow = min(tile * 16 + r, a.N - 1);
+    const uint32_t* pkrow = a.pk + (int64_t)nrow * (a.K >> 3);
+    const uint16_t* scrow = a.sc + (int64_t)nrow * a.groups_per_row;
+#pragma unroll
+    for (int i = 0; i < NST; ++i) {
+      const int g0 = ((s0 + i) * 4 + c) * VPL;
+#pragma unroll
+      for (int v = 0; v < VPL; ++v) wv[tp][i][v] = *reinterpret_cast<const uint4*>(pkrow + 4 * (g0 + v));
+      if (G32) {
+        sv[tp][i] = *reinterpret_cast<const uint32_t*>(scrow + g0);
+      } else {
+        sv[tp][i] = (uint32_t)scrow[g0 / a.group_chunks] | ((uint32_t)scrow[(g0 + 1) / a.group_chunks] << 16);
+      }
+    }
+  }
+
+  // 3. x -> LDS, barrier
+  uint4* xdst = reinterpret_cast<uint4*>(lds);
+#pragma unroll
+  for (int i = 0; i < XPT; ++i) xdst[xi[i]] = xv[i];
+  __syncthreads();
+
+  uint32_t kM = 0x000F000Fu, kO = 0x43004300u;
+  asm volatile("" : "+v"(kM), "+v"(kO));
+  floatx4 acc[TPW];
+  const int plane = a.M * a.K;
+  const uint16_t* xrow = lds + min(r, a.M - 1) * a.K;
+#pragma unroll
+  for (int tp = 0; tp < TPW; ++tp) {
+    acc[tp] = floatx4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int i = 0; i < NST; ++i) {
+#pragma unroll
+      for (int v = 0; v < VPL; ++v) {
+        const int g = ((s0 + i) * 4 + c) * VPL + v;
+        const uint32_t slo = v == 0 ? (sv[tp][i] & 0xffffu) : (sv[tp][i] >> 16);
+        const uint32_t shi = slo << 16;
+        const float cneg = -136.0f * __uint_as_float(shi);
+        const uint16_t* xr = xrow + 32 * g;
+        const uint32_t wj[4] = {wv[tp][i][v].x, wv[tp][i][v].y, wv[tp][i][v].z, wv[tp][i][v].w};
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          const bf16x8 bb = dequant8(wj[j], slo, shi, cneg, kM, kO);
+#pragma unroll
+          for (int t = 0; t < NT; ++t)
+            mfma_acc(acc[tp], *reinterpret_cast<const bf16x8*>(xr + t * plane + 8 * j), bb);
+        }
+      }
+    }
+  }
+  mfma_drain<TPW>(acc);
+
+  float* red = reinterpret_cast<float*>(lds + NT * plane);  // [TPW][waves][4][16]
+  if (c == 0) {
+#pragma unroll
+    for (int tp = 0; tp < TPW; ++tp)
+#pragma unroll
+      for (int i = 0; i < 4; ++i) red[((tp * nwaves + wave) * 4 + i) * 16 + r] = acc[tp][i];
+  }
+  __syncthreads();
+  if ((int)threadIdx.x < 16 * 4 * TPW) {
+    const int tp = threadIdx.x >> 6, m = (threadIdx.x >> 4) & 3, rr = threadIdx.x & 15;
+    const int n = ((int)blockIdx.x * TPW + tp) * 16 + rr;
+    if (m < a.M && n < a.N) {
+      float v = 0.f;
+      for (int w = 0; w < nwaves; ++w) v += red[((tp * nwaves + w) * 4 + m) * 16 + rr];
+      if (a.y_f32) reinterpret_cast<float*>(a.y)[(int64_t)m * a.N + n] = v;
+      else reinterpret_cast<uint16_t*>(a.y)[(int64_t)m * a.N + n] = (uint16_t)f32_to_bf16_rne(v);
+    }
+  }
+}
+
+// ---------------------------------------------------------------- GEMV, streaming variant
+// One workgroup per 16-row tile, W waves splitting K into equal ranges of
+// CPW chunks of NST steps.  Each wave streams its range with two register
+// buffers: the loads of chunk q+1 are issued before chunk q is dequantized,
+// and every load is unconditional in a straight-line loop body (the final
+// chunk is peeled), so the compiler's wait counts stay exact and the next
+// chunk is in flight during the current one's VALU work.  x is staged in LDS
+// as in gemv_fast_kernel.
+template <int NST>
+struct SChunk {
+  uint4 w[NST][VPL];
+  uint32_t s[NST];
+};
+
+template <int NT, int NST, int XPT, bool G32>
+__global__ void __launch_bounds__(1024) gemv_stream_kernel(GemvArgs a, int cpw) {
+  extern __shared__ __attribute__((aligned(16))) uint16_t lds[];
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int nwaves = blockDim.x >> 6;
+  const int r = lane & 15;
+  const int c = lane >> 4;
+  const int n0 = blockIdx.x * 16;
+  const int sw0 = wave * cpw * NST;  // first step of this wave
+
+  const int nvec = (NT * a.M * a.K) >> 3;
+  const uint4* xsrc = reinterpret_cast<const uint4*>(a.x);
+  uint4 xv[XPT];
+  int xi[XPT];
+#pragma unroll
+  for (int i = 0; i < XPT; ++i) {
+    xi[i] = min((int)threadIdx.x + i * (int)blockDim.x, nvec - 1);
+    xv[i] = xsrc[xi[i]];
+  }
+
+  const int nrow = min(n0 + r, a.N - 1);
+  const uint32_t* pkrow = a.pk + (int64_t)nrow * (a.K >> 3);
+  const uint16_t* scrow = a.sc + (int64_t)nrow * a.groups_per_row;
+  auto load = [&](SChunk<NST>& b, int q) {
+#pragma unroll
+    for (int i = 0; i < NST; ++i) {
+      const int g0 = ((sw0 + q * NST + i) * 4 + c) * VPL;
+#pragma unroll
+      for (int v = 0; v < VPL; ++v) b.w[i][v] = *reinterpret_cast<const uint4*>(pkrow + 4 * (g0 + v));
+      if (G32) b.s[i] = *reinterpret_cast<const uint32_t*>(scrow + g0);
+      else b.s[i] = (uint32_t)scrow[g0 / a.group_chunks] | ((uint32_t)scrow[(g0 + 1) / a.group_chunks] << 16);
+    }
+  };
+  SChunk<NST> bA, bB;
+  load(bA, 0);
+
+  uint4* xdst = reinterpret_cast<uint4*>(lds);
+#pragma unroll
+  for (int i = 0; i < XPT; ++i) xdst[xi[i]] = xv[i];
+  __syncthreads();
+
+  uint32_t kM = 0x000F000Fu, kO = 0x43004300u;
+  asm volatile("" : "+v"(kM), "+v"(kO));
+  floatx4 acc[1] = {floatx4{0.f, 0.f, 0.f, 0.f}};
+  const int plane = a.M * a.K;
+  const uint16_t* xrow = lds + min(r, a.M - 1) * a.K;
+  auto compute = [&](const SChunk<NST>& b, int q) {
+#pragma unroll
+    for (int i = 0; i < NST; ++i) {
+#pragma unroll
+      for (int v = 0; v < VPL; ++v) {
+        const int g = ((sw0 + q * NST + i) * 4 + c) * VPL + v;
+        const uint32_t slo = v == 0 ? (b.s[i] & 0xffffu) : (b.s[i] >> 16);
+        const uint32_t shi = slo << 16;
+        const float cneg = -136.0f * __uint_as_float(shi);
+        const uint16_t* xr = xrow + 32 * g;
+        const uint32_t wj[4] = {b.w[i][v].x, b.w[i][v].y, b.w[i][v].z, b.w[i][v].w};
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          const bf16x8 bb = dequant8(wj[j], slo, shi, cneg, kM, kO);
+#pragma unroll
+          for (int t = 0; t < NT; ++t)
+            mfma_acc(acc[0], *reinterpret_cast<const bf16x8*>(xr + t * plane + 8 * j), bb);
+        }
+      }
+    }
+    mfma_drain<1>(acc);
+  };
+  // sched_barrier(0) keeps the scheduler from sinking the next chunk's loads
+  // into the current chunk's compute (it would then wait for them).
+  int q = 0;
+  for (; q + 2 < cpw; q += 2) {
+    load(bB, q + 1);
+    __builtin_amdgcn_sched_barrier(0);
+    compute(bA, q);
+    __builtin_amdgcn_sched_barrier(0);
+    load(bA, q + 2);
+    __builtin_amdgcn_sched_barrier(0);
+    compute(bB, q + 1);
+    __builtin_amdgcn_sched_barrier(0);
+  }
+  if (q + 1 < cpw) {
+    load(bB, q + 1);
+    __builtin_amdgcn_sched_barrier(0);
+    compute(bA, q);
+    __builtin_amdgcn_sched_barrier(0);
+    compute(bB, q + 1);
+  } else {
+    compute(bA, q);
+  }
+  mfma_drain<1>(acc);
+
+  if (nwaves == 1) {
+    if (c == 0 && r < 16) {
+#pragma unroll
+      for (int m = 0; m < 4; ++m) {
+        const int n = n0 + r;
+        if (m < a.M && n < a.N) {
+          if (a.y_f32) reinterpret_cast<float*>(a.y)[(int64_t)m * a.N + n] = acc[0][m];
+          else reinterpret_cast<uint16_t*>(a.y)[(int64_t)m * a.N + n] = (uint16_t)f32_to_bf16_rne(acc[0][m]);
+        }
+      }
+    }
+    return;
+  }
+  float* red = reinterpret_cast<float*>(lds + NT * plane);
+  if (c == 0) {
+#pragma unroll
+    for (int i = 0; i < 4; ++i) red[(wave * 4 + i) * 16 + r] = acc[0][i];
   }
   __syncthreads();
   if ((int)threadIdx.x < 16 * a.M) {
@@ -489,24 +764,192 @@ hipError_t w4l_fill_zero(void* p, int64_t bytes, hipStream_t st) {
 
 
 bool w4l_gemv_ok(int64_t M, int64_t K, int nterms) {
-  return M >= 1 && M <= 4 && (int64_t)nterms * M * K * 2 <= 65536;
+  return M >= 1 && M <= 4 && (int64_t)nterms * M * K * 2 + 16 * 4 * 16 * 4 <= 65536;
 }
 
 int w4l_gemv_waves(int64_t N, int64_t K) {
-  const int64_t steps = (K + w4k::KSTEP - 1) / w4k::KSTEP;
-  const int64_t tiles = (N + 15) / 16;
-  int64_t w = (steps + w4k::SMAX - 1) / w4k::SMAX;      // every wave holds <= SMAX steps
-  const int64_t occ = (2048 + tiles - 1) / tiles;        // >= ~2048 waves in flight
-  if (occ > w) w = occ;
-  if (w > steps) w = steps;
+  const int64_t steps = (K + w4k::GSTEP - 1) / w4k::GSTEP;
+  int64_t w = (steps + w4k::SPW - 1) / w4k::SPW;  // every wave holds <= SPW steps
   if (w > 16) w = 16;
   if (w < 1) w = 1;
+  (void)N;
   return (int)w;
+}
+
+// Straight-line GEMV plan: steps per wave NST (exact divisor of the step
+// count, in the order below) and x vectors per thread XPT (power of two <= 8).
+bool w4l_gemv_fast_plan(int64_t M, int64_t N, int64_t K, int nterms, int* nst_out, int* waves_out,
+                        int* xpt_out, int* tpw_out) {
+  if (K % w4k::GSTEP != 0) return false;
+  const int64_t steps = K / w4k::GSTEP;
+  // measured order on the 12B / 1B decode shapes (K = 1536..15360): five steps per
+  // wave streams best when it divides K/256, then two, four, one
+  static const int pref[] = {5, 2, 4, 1, 3, 6};
+  int nst = 0, waves = 0;
+  // W4A16_GEMV_NST=<1..6>: tuning override of the steps per wave, when it divides
+  if (const char* e = getenv("W4A16_GEMV_NST")) {
+    const int p = atoi(e);
+    if (p >= 1 && p <= 6 && steps % p == 0 && steps / p <= 16) { nst = p; waves = (int)(steps / p); }
+  }
+  for (int p : pref) {
+    if (nst) break;
+    if (steps % p == 0 && steps / p <= 16) { nst = p; waves = (int)(steps / p); break; }
+  }
+  if (!nst) return false;
+  // one 16-row tile per workgroup; two (W4A16_GEMV_TPW=2) measured slower on
+  // every decode shape but stays available for tuning
+  int tpw = 1;
+  if (const char* e = getenv("W4A16_GEMV_TPW")) tpw = atoi(e) == 2 ? 2 : 1;
+  const int64_t nvec = (int64_t)nterms * M * K / 8;
+  const int64_t per = (nvec + 64 * waves - 1) / (64 * waves);
+  int xpt = 1;
+  while (xpt < per) xpt *= 2;
+  if (xpt > 8) return false;
+  *nst_out = nst;
+  *waves_out = waves;
+  *xpt_out = xpt;
+  *tpw_out = tpw;
+  return true;
+}
+
+// Streaming GEMV plan (opt-in with W4A16_GEMV_STREAM): waves per tile W,
+// chunk steps NST, chunks per wave CPW with W * CPW * NST == K / GSTEP.  Few
+// tiles -> more waves per tile.  W4A16_GEMV_W / W4A16_GEMV_NST override.
+bool w4l_gemv_stream_plan(int64_t M, int64_t N, int64_t K, int nterms, int* w_out, int* nst_out,
+                          int* cpw_out, int* xpt_out) {
+  if (K % w4k::GSTEP != 0) return false;
+  const int64_t steps = K / w4k::GSTEP;
+  const int64_t tiles = (N + 15) / 16;
+  int64_t want_w = (2048 + tiles - 1) / tiles;  // >= ~2048 waves in the grid
+  if (want_w > 16) want_w = 16;
+  if (const char* e = getenv("W4A16_GEMV_W")) want_w = atoi(e);
+  int pref_nst = 3;
+  if (const char* e = getenv("W4A16_GEMV_NST")) pref_nst = atoi(e);
+  int w = 0, nst = 0;
+  for (int64_t cw = want_w < 1 ? 1 : want_w; cw <= 16 && !w; ++cw)
+    if (steps % cw == 0) w = (int)cw;
+  if (!w) return false;
+  const int64_t per = steps / w;
+  static const int order[] = {3, 4, 2, 5, 6, 1};
+  if (pref_nst >= 1 && pref_nst <= 6 && per % pref_nst == 0) nst = pref_nst;
+  for (int o : order) {
+    if (nst) break;
+    if (per % o == 0) nst = o;
+  }
+  const int64_t nvec = (int64_t)nterms * M * K / 8;
+  const int64_t xper = (nvec + 64 * w - 1) / (64 * w);
+  int xpt = 1;
+  while (xpt < xper) xpt *= 2;
+  if (xpt > 8) return false;
+  *w_out = w;
+  *nst_out = nst;
+  *cpw_out = (int)(per / nst);
+  *xpt_out = xpt;
+  return true;
 }
 
 hipError_t w4l_gemv(const uint16_t* x_planes, int nterms, const int32_t* pk, const uint16_t* sc,
                     void* y, int y_f32, int64_t M, int64_t N, int64_t K, int32_t group,
                     hipStream_t st) {
+  if (getenv("W4A16_GEMV_STREAM")) {
+    int w, nst, cpw, xpt;
+    if (w4l_gemv_stream_plan(M, N, K, nterms, &w, &nst, &cpw, &xpt)) {
+      w4k::GemvArgs a;
+      a.x = x_planes;
+      a.pk = reinterpret_cast<const uint32_t*>(pk);
+      a.sc = sc;
+      a.y = y;
+      a.M = (int)M;
+      a.N = (int)N;
+      a.K = (int)K;
+      a.group_chunks = group / 32;
+      a.groups_per_row = (int)(K / group);
+      a.y_f32 = y_f32;
+      a.steps = (int)(K / w4k::GSTEP);
+      const size_t lds = (size_t)nterms * M * K * 2 + (size_t)w * 4 * 16 * 4;
+      const dim3 grid((unsigned)((N + 15) / 16)), block(64 * w);
+      const bool g32 = group == 32;
+#define W4_ST(NT_, NST_, XPT_)                                                                             \
+  do {                                                                                                     \
+    if (g32) hipLaunchKernelGGL((w4k::gemv_stream_kernel<NT_, NST_, XPT_, true>), grid, block, lds, st, a, cpw); \
+    else hipLaunchKernelGGL((w4k::gemv_stream_kernel<NT_, NST_, XPT_, false>), grid, block, lds, st, a, cpw);    \
+  } while (0)
+#define W4_ST_X(NT_, NST_)                 \
+  switch (xpt) {                           \
+    case 1: W4_ST(NT_, NST_, 1); break;    \
+    case 2: W4_ST(NT_, NST_, 2); break;    \
+    case 4: W4_ST(NT_, NST_, 4); break;    \
+    default: W4_ST(NT_, NST_, 8); break;   \
+  }
+#define W4_ST_N(NT_)                       \
+  switch (nst) {                           \
+    case 1: W4_ST_X(NT_, 1); break;        \
+    case 2: W4_ST_X(NT_, 2); break;        \
+    case 3: W4_ST_X(NT_, 3); break;        \
+    case 4: W4_ST_X(NT_, 4); break;        \
+    case 5: W4_ST_X(NT_, 5); break;        \
+    default: W4_ST_X(NT_, 6); break;       \
+  }
+      if (nterms == 1) { W4_ST_N(1) } else { W4_ST_N(3) }
+#undef W4_ST_N
+#undef W4_ST_X
+#undef W4_ST
+      return hipGetLastError();
+    }
+  }
+  {
+    int nst, waves, xpt, tpw;
+    if (w4l_gemv_fast_plan(M, N, K, nterms, &nst, &waves, &xpt, &tpw)) {
+      w4k::GemvArgs a;
+      a.x = x_planes;
+      a.pk = reinterpret_cast<const uint32_t*>(pk);
+      a.sc = sc;
+      a.y = y;
+      a.M = (int)M;
+      a.N = (int)N;
+      a.K = (int)K;
+      a.group_chunks = group / 32;
+      a.groups_per_row = (int)(K / group);
+      a.y_f32 = y_f32;
+      a.steps = (int)(K / w4k::GSTEP);
+      const int64_t tiles = (N + 15) / 16;
+      const size_t lds = (size_t)nterms * M * K * 2 + (size_t)tpw * waves * 4 * 16 * 4;
+      const dim3 grid((unsigned)((tiles + tpw - 1) / tpw)), block(64 * waves);
+      const bool g32 = group == 32;
+#define W4_FAST(NT_, NST_, XPT_, TPW_)                                                                          \
+  do {                                                                                                          \
+    if (g32) hipLaunchKernelGGL((w4k::gemv_fast_kernel<NT_, NST_, XPT_, TPW_, true>), grid, block, lds, st, a); \
+    else hipLaunchKernelGGL((w4k::gemv_fast_kernel<NT_, NST_, XPT_, TPW_, false>), grid, block, lds, st, a);    \
+  } while (0)
+#define W4_FAST_T(NT_, NST_, XPT_)                        \
+  do {                                                    \
+    if (tpw == 2) W4_FAST(NT_, NST_, XPT_, 2);            \
+    else W4_FAST(NT_, NST_, XPT_, 1);                     \
+  } while (0)
+#define W4_FAST_X(NT_, NST_)                    \
+  switch (xpt) {                                \
+    case 1: W4_FAST_T(NT_, NST_, 1); break;     \
+    case 2: W4_FAST_T(NT_, NST_, 2); break;     \
+    case 4: W4_FAST_T(NT_, NST_, 4); break;     \
+    default: W4_FAST_T(NT_, NST_, 8); break;    \
+  }
+#define W4_FAST_N(NT_)                         \
+  switch (nst) {                               \
+    case 1: W4_FAST_X(NT_, 1); break;          \
+    case 2: W4_FAST_X(NT_, 2); break;          \
+    case 3: W4_FAST_X(NT_, 3); break;          \
+    case 4: W4_FAST_X(NT_, 4); break;          \
+    case 5: W4_FAST_X(NT_, 5); break;          \
+    default: W4_FAST_X(NT_, 6); break;         \
+  }
+      if (nterms == 1) { W4_FAST_N(1) } else { W4_FAST_N(3) }
+#undef W4_FAST_N
+#undef W4_FAST_X
+#undef W4_FAST_T
+#undef W4_FAST
+      return hipGetLastError();
+    }
+  }
   w4k::GemvArgs a;
   a.x = x_planes;
   a.pk = reinterpret_cast<const uint32_t*>(pk);
@@ -518,12 +961,11 @@ hipError_t w4l_gemv(const uint16_t* x_planes, int nterms, const int32_t* pk, con
   a.group_chunks = group / 32;
   a.groups_per_row = (int)(K / group);
   a.y_f32 = y_f32;
-  a.steps = (int)((K + w4k::KSTEP - 1) / w4k::KSTEP);
+  a.steps = (int)((K + w4k::GSTEP - 1) / w4k::GSTEP);
   const int waves = w4l_gemv_waves(N, K);
-  const size_t xb = (size_t)nterms * M * K * 2, rb = (size_t)waves * 4 * 16 * 4;
-  const size_t lds = xb > rb ? xb : rb;
+  const size_t lds = (size_t)nterms * M * K * 2 + (size_t)waves * 4 * 16 * 4;
   const dim3 grid((unsigned)((N + 15) / 16)), block(64 * waves);
-  const bool kfull = (K % w4k::KSTEP) == 0, g32 = group == 32;
+  const bool kfull = (K % w4k::GSTEP) == 0, g32 = group == 32;
 #define W4_GEMV(NT_, KF_, G_) \
   hipLaunchKernelGGL((w4k::gemv_kernel<NT_, KF_, G_>), grid, block, lds, st, a)
   if (nterms == 1) {

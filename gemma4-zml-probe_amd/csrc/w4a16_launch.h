@@ -21,6 +21,8 @@ W4Plan w4l_plan(int64_t M, int64_t N, int64_t K, int nterms);
 // Decode GEMV path (M <= 4, x planes fit in 64 KiB of LDS).
 bool w4l_gemv_ok(int64_t M, int64_t K, int nterms);
 int w4l_gemv_waves(int64_t N, int64_t K);
+bool w4l_gemv_stream_plan(int64_t M, int64_t N, int64_t K, int nterms, int* w, int* nst, int* cpw, int* xpt);
+bool w4l_gemv_fast_plan(int64_t M, int64_t N, int64_t K, int nterms, int* nst, int* waves, int* xpt, int* tpw);
 hipError_t w4l_gemv(const uint16_t* x_planes, int nterms, const int32_t* pk, const uint16_t* sc,
                     void* y, int y_f32, int64_t M, int64_t N, int64_t K, int32_t group,
                     hipStream_t st);

@@ -414,3 +414,50 @@ def test_graph_capture_replays_match_eager():
         torch.cuda.synchronize()
         assert torch.equal(y.view(torch.int32), ref.view(torch.int32)), rep
         del junk
+
+
+@pytest.mark.parametrize("K,N", [(3840, 512), (15360, 256), (4096, 64)])
+def test_gemv_stream_plans(K, N, monkeypatch):
+    """The streaming GEMV under every (waves per tile, steps per chunk) plan the
+    tuning knobs allow: 1..15 chunks per wave, odd and even counts, so the
+    double-buffered loop, its peeled tail and the cross-wave reduction all run."""
+    _, pk, sc = o.synth_weights(N, K, 41)
+    x = o.synth_x(1, K, 42)
+    w = o.dequant(pk, sc)
+    ref32 = o.matmul_f32(x, w)
+    steps = K // 256
+    seen = set()
+    for W in (1, 2, 3, 4, 5, 8, 15, 16):
+        if steps % W:
+            continue
+        for nst in (1, 2, 3, 4, 5, 6):
+            if (steps // W) % nst:
+                continue
+            monkeypatch.setenv("W4A16_GEMV_STREAM", "1")
+            monkeypatch.setenv("W4A16_GEMV_W", str(W))
+            monkeypatch.setenv("W4A16_GEMV_NST", str(nst))
+            say(f"stream plan K={K} N={N} W={W} NST={nst} CPW={steps // W // nst}")
+            y = gpu_linear(x, pk, sc, "f32")
+            check_f32(y, x, w, K, ref32)
+            seen.add(steps // W // nst)
+    assert max(seen) >= 3 and len(seen) >= 3, seen
+
+
+@pytest.mark.parametrize("N", [16, 48, 400, 30720])
+@pytest.mark.parametrize("tpw", ["1", "2"])
+def test_gemv_tiles_per_workgroup(N, tpw, monkeypatch):
+    """The straight-line GEMV with one or two 16-row tiles per workgroup,
+    including odd tile counts (the last workgroup's second tile is a clamped
+    duplicate that must not be written) and ragged N."""
+    K = 3840
+    monkeypatch.setenv("W4A16_GEMV_TPW", tpw)
+    _, pk, sc = o.synth_weights(N, K, 43)
+    x = o.synth_x(1, K, 44)
+    w = o.dequant(pk, sc)
+    ref32 = o.matmul_f32(x, w)
+    say(f"tiles per workgroup {tpw}: N={N}")
+    y = gpu_linear(x, pk, sc, "f32")
+    check_f32(y, x, w, K, ref32)
+    yb = gpu_linear(x, pk, sc, "bf16")
+    _, mag = o.matmul_f64(x, w)
+    check_bf16(yb, ref32, mag, K)
