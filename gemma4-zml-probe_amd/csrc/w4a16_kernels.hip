@@ -20,6 +20,8 @@
 #include <stdint.h>
 #include <stdlib.h>
 
+#include <type_traits>
+
 namespace w4k {
 
 typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
@@ -53,21 +55,21 @@ __device__ __forceinline__ uint32_t f32_to_bf16_rne(float f) {
 // interlock a DOT result read by another VALU instruction (3 wait states):
 // all dots are issued before the first conversion, so every conversion reads
 // a dot result at least 3 instructions old.  The VALU -> MFMA wait states are
-// issued by mfma_acc.
+// issued by mfma_acc.  Twelve temporaries: the shifts land in the pair
+// registers and each conversion overwrites its first dot result, which keeps
+// the decode kernels at <= 80 VGPRs (six waves per SIMD).
 // kM = 0x000F000F and kO = 0x43004300 come in VGPRs (VOP3 takes no literals).
 __device__ __forceinline__ bf16x8 dequant8(uint32_t w, uint32_t slo, uint32_t shi, float c,
                                            uint32_t kM, uint32_t kO) {
-  uint32_t r0, r1, r2, r3, t, p0, p1, p2, p3;
-  float d0, d1, d2, d3, d4, d5, d6, d7;
-  // v_bitop3_b32 with truth table 0xEA computes (a & b) | c; on gfx950 it
-  // issues at twice the rate of v_and_or_b32.
+  uint32_t p0, p1, p2, p3, d0, d1, d2, d3, d4, d5, d6, d7;
+  // v_bitop3_b32 with truth table 0xEA computes (a & b) | c.
   asm("v_bitop3_b32 %[p0], %[w], %[km], %[ko] bitop3:0xea\n\t"
-      "v_lshrrev_b32 %[t], 4, %[w]\n\t"
-      "v_bitop3_b32 %[p1], %[t], %[km], %[ko] bitop3:0xea\n\t"
-      "v_lshrrev_b32 %[t], 8, %[w]\n\t"
-      "v_bitop3_b32 %[p2], %[t], %[km], %[ko] bitop3:0xea\n\t"
-      "v_lshrrev_b32 %[t], 12, %[w]\n\t"
-      "v_bitop3_b32 %[p3], %[t], %[km], %[ko] bitop3:0xea\n\t"
+      "v_lshrrev_b32 %[p1], 4, %[w]\n\t"
+      "v_lshrrev_b32 %[p2], 8, %[w]\n\t"
+      "v_lshrrev_b32 %[p3], 12, %[w]\n\t"
+      "v_bitop3_b32 %[p1], %[p1], %[km], %[ko] bitop3:0xea\n\t"
+      "v_bitop3_b32 %[p2], %[p2], %[km], %[ko] bitop3:0xea\n\t"
+      "v_bitop3_b32 %[p3], %[p3], %[km], %[ko] bitop3:0xea\n\t"
       "v_dot2_f32_bf16 %[d0], %[p0], %[slo], %[c]\n\t"
       "v_dot2_f32_bf16 %[d1], %[p1], %[slo], %[c]\n\t"
       "v_dot2_f32_bf16 %[d2], %[p2], %[slo], %[c]\n\t"
@@ -76,20 +78,19 @@ __device__ __forceinline__ bf16x8 dequant8(uint32_t w, uint32_t slo, uint32_t sh
       "v_dot2_f32_bf16 %[d5], %[p1], %[shi], %[c]\n\t"
       "v_dot2_f32_bf16 %[d6], %[p2], %[shi], %[c]\n\t"
       "v_dot2_f32_bf16 %[d7], %[p3], %[shi], %[c]\n\t"
-      "v_cvt_pk_bf16_f32 %[r0], %[d0], %[d1]\n\t"
-      "v_cvt_pk_bf16_f32 %[r1], %[d2], %[d3]\n\t"
-      "v_cvt_pk_bf16_f32 %[r2], %[d4], %[d5]\n\t"
-      "v_cvt_pk_bf16_f32 %[r3], %[d6], %[d7]"
-      : [r0] "=&v"(r0), [r1] "=&v"(r1), [r2] "=&v"(r2), [r3] "=&v"(r3), [t] "=&v"(t),
-        [p0] "=&v"(p0), [p1] "=&v"(p1), [p2] "=&v"(p2), [p3] "=&v"(p3),
+      "v_cvt_pk_bf16_f32 %[d0], %[d0], %[d1]\n\t"
+      "v_cvt_pk_bf16_f32 %[d2], %[d2], %[d3]\n\t"
+      "v_cvt_pk_bf16_f32 %[d4], %[d4], %[d5]\n\t"
+      "v_cvt_pk_bf16_f32 %[d6], %[d6], %[d7]"
+      : [p0] "=&v"(p0), [p1] "=&v"(p1), [p2] "=&v"(p2), [p3] "=&v"(p3),
         [d0] "=&v"(d0), [d1] "=&v"(d1), [d2] "=&v"(d2), [d3] "=&v"(d3),
         [d4] "=&v"(d4), [d5] "=&v"(d5), [d6] "=&v"(d6), [d7] "=&v"(d7)
       : [w] "v"(w), [slo] "v"(slo), [shi] "v"(shi), [c] "v"(c), [km] "v"(kM), [ko] "v"(kO));
   u32x4 r;
-  r[0] = r0;
-  r[1] = r1;
-  r[2] = r2;
-  r[3] = r3;
+  r[0] = d0;
+  r[1] = d2;
+  r[2] = d4;
+  r[3] = d6;
   return __builtin_bit_cast(bf16x8, r);
 }
 
@@ -708,6 +709,170 @@ __global__ void __launch_bounds__(1024) gemv_stream_kernel(GemvArgs a, int cpw) 
   }
 }
 
+// ---------------------------------------------------------------- skinny / prefill linear
+// M > 4, bf16 x, K % 256 == 0.  A workgroup of 4 waves owns 64 rows of W (16 per
+// wave) and 16*MT rows of x, and walks K in chunks of 256 columns.  Per chunk:
+//   - x[16*MT][256] is staged in LDS (double buffered; the global loads of the
+//     chunk after next are issued two chunks ahead, into a register ring),
+//   - each wave expands its 16 rows x 256 columns of W once in registers and
+//     feeds every 16x32 weight fragment to MT MFMAs (one per 16 rows of x),
+//   - weights are prefetched P chunks ahead in a register ring.
+// Every load is unconditional (chunk index clamped to the last chunk), and the
+// main loop is unrolled by P so that the ring slots are compile-time registers;
+// together these keep the compiler's wait counts exact.  Rows of x past M
+// duplicate row M-1 and rows of W past N duplicate row N-1; neither is stored.
+// Grid: (ceil(N/64), ceil(M/(16*MT))); large M re-expands W once per 16*MT rows.
+struct SkinnyArgs {
+  const uint16_t* x;  // [M][K] bf16
+  const uint32_t* pk;
+  const uint16_t* sc;
+  void* y;
+  int M, N, K;
+  int group_chunks;    // group / 32
+  int groups_per_row;  // K / group
+  int y_f32;
+  int nk;              // K / 256
+};
+
+constexpr int SK_P = 4;  // weight prefetch depth (chunks); even, for the two-slot x ring
+
+template <int MT, bool G32>
+__global__ void __launch_bounds__(256) skinny_kernel(SkinnyArgs a) {
+  constexpr int P = SK_P;
+  constexpr int XPAD = 8;  // halves of padding per LDS row
+  __shared__ __attribute__((aligned(16))) uint16_t xs[2][16 * MT][256 + XPAD];
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int r = lane & 15, c = lane >> 4;
+  const int m0 = blockIdx.y * (16 * MT);
+  const int n = min((int)blockIdx.x * 64 + 16 * wave + r, a.N - 1);
+  const uint32_t* pkrow = a.pk + (int64_t)n * (a.K >> 3);
+  const uint16_t* scrow = a.sc + (int64_t)n * a.groups_per_row;
+
+  // weight ring: chunk k -> slot k % P; lane (r, c) holds the 32-column chunks
+  // 8k + 2c and 8k + 2c + 1 of its row (two 16-byte vectors) and their scales.
+  uint4 wv[P][2];
+  uint32_t sv[P];
+  auto wload = [&](auto slot_c, int k) __attribute__((always_inline)) {
+    constexpr int slot = decltype(slot_c)::value;
+    const int g0 = (k * 4 + c) * 2;
+    wv[slot][0] = *reinterpret_cast<const uint4*>(pkrow + 4 * g0);
+    wv[slot][1] = *reinterpret_cast<const uint4*>(pkrow + 4 * g0 + 4);
+    if (G32) sv[slot] = *reinterpret_cast<const uint32_t*>(scrow + g0);
+    else sv[slot] = (uint32_t)scrow[g0 / a.group_chunks] | ((uint32_t)scrow[(g0 + 1) / a.group_chunks] << 16);
+  };
+
+  // x staging: thread t moves vectors t + 256 i (i < 2*MT) of the [16*MT][256] chunk.
+  // The register ring is an ext_vector value (not an array) so that it never lives
+  // in scratch memory.
+  constexpr int XV = 2 * MT;
+  typedef uint32_t xvec_t __attribute__((ext_vector_type(4 * XV)));
+  auto xload = [&](xvec_t& xr, int k) __attribute__((always_inline)) {
+#pragma unroll
+    for (int i = 0; i < XV; ++i) {
+      const int v = (int)threadIdx.x + 256 * i;
+      const int row = v >> 5, col = (v & 31) * 8;
+      const int m = min(m0 + row, a.M - 1);
+      const u32x4 t = *reinterpret_cast<const u32x4*>(a.x + (int64_t)m * a.K + k * 256 + col);
+      xr[4 * i] = t[0];
+      xr[4 * i + 1] = t[1];
+      xr[4 * i + 2] = t[2];
+      xr[4 * i + 3] = t[3];
+    }
+  };
+  auto xstore = [&](const xvec_t& xr, int buf) __attribute__((always_inline)) {
+#pragma unroll
+    for (int i = 0; i < XV; ++i) {
+      const int v = (int)threadIdx.x + 256 * i;
+      const int row = v >> 5, col = (v & 31) * 8;
+      *reinterpret_cast<u32x4*>(&xs[buf][row][col]) = u32x4{xr[4 * i], xr[4 * i + 1], xr[4 * i + 2], xr[4 * i + 3]};
+    }
+  };
+
+  // prologue: x chunk 0 -> LDS buffer 0, x chunk 1 -> register slot 1, weights 0..P-1
+  xvec_t xreg0, xreg1;
+  xload(xreg0, 0);
+  xload(xreg1, min(1, a.nk - 1));
+  wload(std::integral_constant<int, 0>{}, 0);
+  wload(std::integral_constant<int, 1>{}, min(1, a.nk - 1));
+  wload(std::integral_constant<int, 2>{}, min(2, a.nk - 1));
+  wload(std::integral_constant<int, 3>{}, min(3, a.nk - 1));
+  xstore(xreg0, 0);
+  __syncthreads();
+
+  uint32_t kM = 0x000F000Fu, kO = 0x43004300u;
+  asm volatile("" : "+v"(kM), "+v"(kO));
+  floatx4 acc[MT];
+#pragma unroll
+  for (int mt = 0; mt < MT; ++mt) acc[mt] = floatx4{0.f, 0.f, 0.f, 0.f};
+
+  auto compute = [&](auto slot_c, int buf) __attribute__((always_inline)) {
+    constexpr int slot = decltype(slot_c)::value;
+#pragma unroll
+    for (int v = 0; v < 2; ++v) {
+      const uint32_t slo = v == 0 ? (sv[slot] & 0xffffu) : (sv[slot] >> 16);
+      const uint32_t shi = slo << 16;
+      const float cneg = -136.0f * __uint_as_float(shi);
+      // every A fragment of this half-chunk first: one LDS round trip
+      bf16x8 xa[4][MT];
+#pragma unroll
+      for (int j = 0; j < 4; ++j)
+#pragma unroll
+        for (int mt = 0; mt < MT; ++mt)
+          xa[j][mt] = *reinterpret_cast<const bf16x8*>(&xs[buf][16 * mt + r][(c * 2 + v) * 32 + 8 * j]);
+      __builtin_amdgcn_sched_barrier(0);
+      const uint32_t wj[4] = {wv[slot][v].x, wv[slot][v].y, wv[slot][v].z, wv[slot][v].w};
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const bf16x8 bb = dequant8(wj[j], slo, shi, cneg, kM, kO);
+#pragma unroll
+        for (int mt = 0; mt < MT; ++mt) mfma_acc(acc[mt], xa[j][mt], bb);
+      }
+    }
+  };
+
+  // chunk k: x of chunk k+2 into register slot k%2 (chunk k left it last
+  // iteration), compute from LDS buffer k%2, weights of chunk k+P into slot k%P,
+  // x of chunk k+1 (register slot (k+1)%2) into LDS buffer (k+1)%2, barrier.
+  auto iter = [&](int k, auto slot_c) __attribute__((always_inline)) {
+    constexpr int p = decltype(slot_c)::value;
+    if constexpr (p % 2 == 0) xload(xreg0, min(k + 2, a.nk - 1));
+    else xload(xreg1, min(k + 2, a.nk - 1));
+    compute(slot_c, k & 1);
+    mfma_drain<MT>(acc);
+    wload(slot_c, min(k + P, a.nk - 1));
+    if constexpr (p % 2 == 0) xstore(xreg1, (k + 1) & 1);
+    else xstore(xreg0, (k + 1) & 1);
+    __syncthreads();
+  };
+  int k = 0;
+  for (; k + P <= a.nk; k += P) {
+    iter(k, std::integral_constant<int, 0>{});
+    iter(k + 1, std::integral_constant<int, 1>{});
+    iter(k + 2, std::integral_constant<int, 2>{});
+    iter(k + 3, std::integral_constant<int, 3>{});
+  }
+  if (k < a.nk) iter(k, std::integral_constant<int, 0>{});
+  if (k + 1 < a.nk) iter(k + 1, std::integral_constant<int, 1>{});
+  if (k + 2 < a.nk) iter(k + 2, std::integral_constant<int, 2>{});
+
+  // D layout: lane (n = r, c) holds D[m = 4c + i][n]
+  const int nout = (int)blockIdx.x * 64 + 16 * wave + r;
+  if (nout < a.N) {
+#pragma unroll
+    for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const int m = m0 + 16 * mt + 4 * c + i;
+        if (m < a.M) {
+          const float v = acc[mt][i];
+          if (a.y_f32) reinterpret_cast<float*>(a.y)[(int64_t)m * a.N + nout] = v;
+          else reinterpret_cast<uint16_t*>(a.y)[(int64_t)m * a.N + nout] = (uint16_t)f32_to_bf16_rne(v);
+        }
+      }
+  }
+}
+
 // K == 0: y = 0 (a kernel rather than a memset, so callers may capture it in a graph).
 __global__ void __launch_bounds__(256) fill_zero_kernel(uint16_t* __restrict__ p, int64_t nhalves) {
   const int64_t stride = (int64_t)gridDim.x * blockDim.x;
@@ -997,10 +1162,44 @@ W4Plan w4l_plan(int64_t M, int64_t N, int64_t K, int nterms) {
   return p;
 }
 
+bool w4l_skinny_ok(int64_t M, int64_t K, int nterms) {
+  return nterms == 1 && M > 4 && K % 256 == 0;
+}
+
+hipError_t w4l_skinny(const uint16_t* x, const int32_t* pk, const uint16_t* sc, void* y, int y_f32,
+                      int64_t M, int64_t N, int64_t K, int32_t group, hipStream_t st) {
+  w4k::SkinnyArgs a;
+  a.x = x;
+  a.pk = reinterpret_cast<const uint32_t*>(pk);
+  a.sc = sc;
+  a.y = y;
+  a.M = (int)M;
+  a.N = (int)N;
+  a.K = (int)K;
+  a.group_chunks = group / 32;
+  a.groups_per_row = (int)(K / group);
+  a.y_f32 = y_f32;
+  a.nk = (int)(K / 256);
+  const int mt = M <= 16 ? 1 : M <= 32 ? 2 : 4;
+  const dim3 grid((unsigned)((N + 63) / 64), (unsigned)((M + 16 * mt - 1) / (16 * mt))), block(256);
+  const bool g32 = group == 32;
+#define W4_SK(MT_)                                                                                   \
+  do {                                                                                               \
+    if (g32) hipLaunchKernelGGL((w4k::skinny_kernel<MT_, true>), grid, block, 0, st, a);            \
+    else hipLaunchKernelGGL((w4k::skinny_kernel<MT_, false>), grid, block, 0, st, a);               \
+  } while (0)
+  if (mt == 1) W4_SK(1);
+  else if (mt == 2) W4_SK(2);
+  else W4_SK(4);
+#undef W4_SK
+  return hipGetLastError();
+}
+
 hipError_t w4l_linear(const uint16_t* x_planes, int nterms, const int32_t* pk, const uint16_t* sc,
                       void* y, int y_f32, int64_t M, int64_t N, int64_t K, int32_t group,
                       hipStream_t st) {
   if (w4l_gemv_ok(M, K, nterms)) return w4l_gemv(x_planes, nterms, pk, sc, y, y_f32, M, N, K, group, st);
+  if (w4l_skinny_ok(M, K, nterms)) return w4l_skinny(x_planes, pk, sc, y, y_f32, M, N, K, group, st);
   const W4Plan p = w4l_plan(M, N, K, nterms);
   w4k::LinearArgs a;
   a.x = x_planes;

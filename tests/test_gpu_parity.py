@@ -304,7 +304,11 @@ def test_linear_c5_prefill(K, N):
 
 @pytest.mark.parametrize("M,N,K,group", [(1, 17, 32, 32), (5, 33, 96, 32), (2, 1, 160, 32),
                                          (3, 48, 256, 64), (1, 64, 512, 128), (4, 24, 384, 128),
-                                         (1, 1, 32, 32)])
+                                         (1, 1, 32, 32),
+                                         # M > 4, K % 256 == 0 (skinny path): chunk counts 1, 2,
+                                         # 3, 5, 7 (prefetch tails), partial row blocks of W and x
+                                         (5, 33, 256, 32), (65, 70, 512, 128), (17, 100, 768, 64),
+                                         (40, 129, 1280, 32), (100, 64, 1792, 256), (7, 16, 256, 256)])
 def test_linear_ragged(M, N, K, group):
     say(f"ragged M={M} N={N} K={K} group={group}")
     _, pk, sc = o.synth_weights(N, K, 55, group)
