@@ -26,6 +26,7 @@ namespace w4k {
 
 typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
 typedef float floatx4 __attribute__((ext_vector_type(4)));
+typedef float floatx16 __attribute__((ext_vector_type(16)));
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 
 constexpr int KSTEP = 128;  // K covered by one wave per step (4 lane groups x 32)
@@ -873,6 +874,188 @@ __global__ void __launch_bounds__(256) skinny_kernel(SkinnyArgs a) {
   }
 }
 
+// ---------------------------------------------------------------- prefill linear (M > 64)
+// bf16 x, K % 64 == 0.  v_mfma_f32_32x32x16_bf16 with the accumulators in AGPRs.
+// A workgroup of 4 waves owns 256 rows of x (staged in LDS, 64 columns per step,
+// double buffered, global loads two steps ahead) and 4 * 32 * TN rows of W; each
+// wave expands its 32 * TN rows of W per step in registers and feeds every
+// 16x32 weight fragment to 8 MFMAs (one per 32 rows of x), so each weight is
+// expanded once per 256 rows of x.
+// Lane layouts (checked on the GPU): A lane l holds A[l % 32][8 (l / 32) + i],
+// B lane l holds B[8 (l / 32) + i][l % 32], D lane l value e holds
+// D[8 (e / 4) + 4 (l / 32) + e % 4][l % 32].  Lane (n, h) of a W block loads the
+// 32 columns [64 s + 32 h, +32) of its row; word j of them feeds MFMA j, whose
+// reduction index kk = 8 h + i is column 64 s + 32 h + 8 j + i, and the A
+// fragment is read from the same columns of x.
+// Workgroup b takes the x block b % mblk and the W block b / mblk: consecutive
+// workgroups (placed on different XCDs) share a W block, and an XCD keeps the
+// same x rows while it walks W.
+__device__ __forceinline__ void mfma32_acc(floatx16& acc, const bf16x8& a, const bf16x8& b) {
+  asm("s_nop 1\n\tv_mfma_f32_32x32x16_bf16 %0, %1, %2, %0" : "+a"(acc) : "v"(a), "v"(b));
+}
+
+struct PrefillArgs {
+  const uint16_t* x;  // [M][K] bf16
+  const uint32_t* pk;
+  const uint16_t* sc;
+  void* y;
+  int M, N, K;
+  int group_chunks;
+  int groups_per_row;
+  int y_f32;
+  int ns;    // K / 64
+  int mblk;  // ceil(M / 256)
+};
+
+template <int TN, int P, bool G32>
+__global__ void __launch_bounds__(256) prefill_kernel(PrefillArgs a) {
+  constexpr int MB = 8;            // 32-row blocks of x per workgroup
+  constexpr int BM = 32 * MB;
+  constexpr int BN = 4 * 32 * TN;
+  constexpr int XPAD = 8;
+  __shared__ __attribute__((aligned(16))) uint16_t xs[2][BM][64 + XPAD];
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int l32 = lane & 31, h = lane >> 5;
+  const int m0 = ((int)blockIdx.x % a.mblk) * BM;
+  const int nw0 = ((int)blockIdx.x / a.mblk) * BN + wave * 32 * TN;
+
+  const uint32_t* pkrow[TN];
+  const uint16_t* scrow[TN];
+#pragma unroll
+  for (int t = 0; t < TN; ++t) {
+    const int n = min(nw0 + 32 * t + l32, a.N - 1);
+    pkrow[t] = a.pk + (int64_t)n * (a.K >> 3);
+    scrow[t] = a.sc + (int64_t)n * a.groups_per_row;
+  }
+  uint4 wv[P][TN];
+  uint32_t sv[P][TN];
+  auto wload = [&](auto slot_c, int s) __attribute__((always_inline)) {
+    constexpr int slot = decltype(slot_c)::value;
+#pragma unroll
+    for (int t = 0; t < TN; ++t) {
+      const int g = 2 * s + h;
+      wv[slot][t] = *reinterpret_cast<const uint4*>(pkrow[t] + 4 * g);
+      sv[slot][t] = scrow[t][G32 ? g : g / a.group_chunks];
+    }
+  };
+  constexpr int XV = BM * 8 / 256;  // 16-byte vectors of the [BM][64] step per thread
+  typedef uint32_t xvec_t __attribute__((ext_vector_type(4 * XV)));
+  auto xload = [&](xvec_t& xr, int s) __attribute__((always_inline)) {
+#pragma unroll
+    for (int i = 0; i < XV; ++i) {
+      const int v = (int)threadIdx.x + 256 * i;
+      const int row = v >> 3, col = (v & 7) * 8;
+      const int m = min(m0 + row, a.M - 1);
+      const u32x4 t = *reinterpret_cast<const u32x4*>(a.x + (int64_t)m * a.K + s * 64 + col);
+      xr[4 * i] = t[0];
+      xr[4 * i + 1] = t[1];
+      xr[4 * i + 2] = t[2];
+      xr[4 * i + 3] = t[3];
+    }
+  };
+  auto xstore = [&](const xvec_t& xr, int buf) __attribute__((always_inline)) {
+#pragma unroll
+    for (int i = 0; i < XV; ++i) {
+      const int v = (int)threadIdx.x + 256 * i;
+      const int row = v >> 3, col = (v & 7) * 8;
+      *reinterpret_cast<u32x4*>(&xs[buf][row][col]) = u32x4{xr[4 * i], xr[4 * i + 1], xr[4 * i + 2], xr[4 * i + 3]};
+    }
+  };
+
+  xvec_t xreg0, xreg1;
+  xload(xreg0, 0);
+  xload(xreg1, min(1, a.ns - 1));
+  wload(std::integral_constant<int, 0>{}, 0);
+  wload(std::integral_constant<int, 1>{}, min(1, a.ns - 1));
+  if constexpr (P > 2) wload(std::integral_constant<int, 2>{}, min(2, a.ns - 1));
+  if constexpr (P > 3) wload(std::integral_constant<int, 3>{}, min(3, a.ns - 1));
+  xstore(xreg0, 0);
+  __syncthreads();
+
+  uint32_t kM = 0x000F000Fu, kO = 0x43004300u;
+  asm volatile("" : "+v"(kM), "+v"(kO));
+  floatx16 acc[MB][TN];
+#pragma unroll
+  for (int i = 0; i < MB; ++i)
+#pragma unroll
+    for (int t = 0; t < TN; ++t) acc[i][t] = floatx16{};
+
+  auto compute = [&](auto slot_c, int buf) __attribute__((always_inline)) {
+    constexpr int slot = decltype(slot_c)::value;
+    uint32_t shi[TN];
+    float cn[TN];
+#pragma unroll
+    for (int t = 0; t < TN; ++t) {
+      shi[t] = sv[slot][t] << 16;
+      cn[t] = -136.0f * __uint_as_float(shi[t]);
+    }
+    bf16x8 xa[2][MB];
+#pragma unroll
+    for (int i = 0; i < MB; ++i) xa[0][i] = *reinterpret_cast<const bf16x8*>(&xs[buf][32 * i + l32][32 * h]);
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      if (j < 3) {
+#pragma unroll
+        for (int i = 0; i < MB; ++i)
+          xa[(j + 1) & 1][i] = *reinterpret_cast<const bf16x8*>(&xs[buf][32 * i + l32][32 * h + 8 * (j + 1)]);
+      }
+      bf16x8 bb[TN];
+#pragma unroll
+      for (int t = 0; t < TN; ++t) {
+        const uint32_t w = j == 0 ? wv[slot][t].x : j == 1 ? wv[slot][t].y : j == 2 ? wv[slot][t].z : wv[slot][t].w;
+        bb[t] = dequant8(w, sv[slot][t], shi[t], cn[t], kM, kO);
+      }
+#pragma unroll
+      for (int i = 0; i < MB; ++i)
+#pragma unroll
+        for (int t = 0; t < TN; ++t) mfma32_acc(acc[i][t], xa[j & 1][i], bb[t]);
+    }
+  };
+
+  auto iter = [&](int s, auto slot_c) __attribute__((always_inline)) {
+    constexpr int p = decltype(slot_c)::value;
+    if constexpr (p % 2 == 0) xload(xreg0, min(s + 2, a.ns - 1));
+    else xload(xreg1, min(s + 2, a.ns - 1));
+    compute(slot_c, s & 1);
+    wload(slot_c, min(s + P, a.ns - 1));
+    if constexpr (p % 2 == 0) xstore(xreg1, (s + 1) & 1);
+    else xstore(xreg0, (s + 1) & 1);
+    __syncthreads();
+  };
+  int s = 0;
+  for (; s + P <= a.ns; s += P) {
+    iter(s, std::integral_constant<int, 0>{});
+    iter(s + 1, std::integral_constant<int, 1>{});
+    if constexpr (P > 2) iter(s + 2, std::integral_constant<int, 2>{});
+    if constexpr (P > 3) iter(s + 3, std::integral_constant<int, 3>{});
+  }
+  if (s < a.ns) iter(s, std::integral_constant<int, 0>{});
+  if constexpr (P > 1) if (s + 1 < a.ns) iter(s + 1, std::integral_constant<int, 1>{});
+  if constexpr (P > 2) if (s + 2 < a.ns) iter(s + 2, std::integral_constant<int, 2>{});
+  // the last MFMAs must finish before their AGPRs are read (16-pass MFMA: >= 18 wait states)
+  asm volatile("s_nop 7\n\ts_nop 7\n\ts_nop 7\n\ts_nop 7" ::: "memory");
+
+#pragma unroll
+  for (int t = 0; t < TN; ++t) {
+    const int n = nw0 + 32 * t + l32;
+    if (n < a.N) {
+#pragma unroll
+      for (int i = 0; i < MB; ++i) {
+        const floatx16 v = acc[i][t];
+#pragma unroll
+        for (int e = 0; e < 16; ++e) {
+          const int m = m0 + 32 * i + 8 * (e >> 2) + 4 * h + (e & 3);
+          if (m < a.M) {
+            if (a.y_f32) reinterpret_cast<float*>(a.y)[(int64_t)m * a.N + n] = v[e];
+            else reinterpret_cast<uint16_t*>(a.y)[(int64_t)m * a.N + n] = (uint16_t)f32_to_bf16_rne(v[e]);
+          }
+        }
+      }
+    }
+  }
+}
+
 // K == 0: y = 0 (a kernel rather than a memset, so callers may capture it in a graph).
 __global__ void __launch_bounds__(256) fill_zero_kernel(uint16_t* __restrict__ p, int64_t nhalves) {
   const int64_t stride = (int64_t)gridDim.x * blockDim.x;
@@ -1195,10 +1378,45 @@ hipError_t w4l_skinny(const uint16_t* x, const int32_t* pk, const uint16_t* sc, 
   return hipGetLastError();
 }
 
+bool w4l_prefill_ok(int64_t M, int64_t K, int nterms) {
+  return nterms == 1 && M > 64 && K % 64 == 0;
+}
+
+hipError_t w4l_prefill(const uint16_t* x, const int32_t* pk, const uint16_t* sc, void* y, int y_f32,
+                       int64_t M, int64_t N, int64_t K, int32_t group, hipStream_t st) {
+  w4k::PrefillArgs a;
+  a.x = x;
+  a.pk = reinterpret_cast<const uint32_t*>(pk);
+  a.sc = sc;
+  a.y = y;
+  a.M = (int)M;
+  a.N = (int)N;
+  a.K = (int)K;
+  a.group_chunks = group / 32;
+  a.groups_per_row = (int)(K / group);
+  a.y_f32 = y_f32;
+  a.ns = (int)(K / 64);
+  a.mblk = (int)((M + 255) / 256);
+  // two W blocks of 32 rows per wave when that still leaves two workgroups per CU
+  const bool tn2 = ((N + 255) / 256) * a.mblk >= 512;
+  const int bn = tn2 ? 256 : 128;
+  const dim3 grid((unsigned)(((N + bn - 1) / bn) * a.mblk)), block(256);
+  const bool g32 = group == 32;
+  if (tn2) {
+    if (g32) hipLaunchKernelGGL((w4k::prefill_kernel<2, 2, true>), grid, block, 0, st, a);
+    else hipLaunchKernelGGL((w4k::prefill_kernel<2, 2, false>), grid, block, 0, st, a);
+  } else {
+    if (g32) hipLaunchKernelGGL((w4k::prefill_kernel<1, 4, true>), grid, block, 0, st, a);
+    else hipLaunchKernelGGL((w4k::prefill_kernel<1, 4, false>), grid, block, 0, st, a);
+  }
+  return hipGetLastError();
+}
+
 hipError_t w4l_linear(const uint16_t* x_planes, int nterms, const int32_t* pk, const uint16_t* sc,
                       void* y, int y_f32, int64_t M, int64_t N, int64_t K, int32_t group,
                       hipStream_t st) {
   if (w4l_gemv_ok(M, K, nterms)) return w4l_gemv(x_planes, nterms, pk, sc, y, y_f32, M, N, K, group, st);
+  if (w4l_prefill_ok(M, K, nterms)) return w4l_prefill(x_planes, pk, sc, y, y_f32, M, N, K, group, st);
   if (w4l_skinny_ok(M, K, nterms)) return w4l_skinny(x_planes, pk, sc, y, y_f32, M, N, K, group, st);
   const W4Plan p = w4l_plan(M, N, K, nterms);
   w4k::LinearArgs a;

@@ -32,6 +32,11 @@ bool w4l_skinny_ok(int64_t M, int64_t K, int nterms);
 hipError_t w4l_skinny(const uint16_t* x, const int32_t* pk, const uint16_t* sc, void* y, int y_f32,
                       int64_t M, int64_t N, int64_t K, int32_t group, hipStream_t st);
 
+// Prefill path (M > 64, bf16 x, K % 64 == 0).
+bool w4l_prefill_ok(int64_t M, int64_t K, int nterms);
+hipError_t w4l_prefill(const uint16_t* x, const int32_t* pk, const uint16_t* sc, void* y, int y_f32,
+                       int64_t M, int64_t N, int64_t K, int32_t group, hipStream_t st);
+
 hipError_t w4l_unpack(const int32_t* pk, int8_t* q, int64_t nwords, hipStream_t st);
 hipError_t w4l_dequant(const int32_t* pk, const uint16_t* sc, uint16_t* w, int64_t N, int64_t K,
                        int32_t group, hipStream_t st);

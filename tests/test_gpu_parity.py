@@ -308,7 +308,11 @@ def test_linear_c5_prefill(K, N):
                                          # M > 4, K % 256 == 0 (skinny path): chunk counts 1, 2,
                                          # 3, 5, 7 (prefetch tails), partial row blocks of W and x
                                          (5, 33, 256, 32), (65, 70, 512, 128), (17, 100, 768, 64),
-                                         (40, 129, 1280, 32), (100, 64, 1792, 256), (7, 16, 256, 256)])
+                                         (40, 129, 1280, 32), (100, 64, 1792, 256), (7, 16, 256, 256),
+                                         # M > 64, K % 64 == 0 (prefill path): partial 256-row x
+                                         # blocks and 128-row W blocks, 1 / 3 / 5 / 32 steps of 64
+                                         (300, 200, 192, 64), (129, 33, 64, 32), (257, 130, 320, 32),
+                                         (70, 300, 2048, 128)])
 def test_linear_ragged(M, N, K, group):
     say(f"ragged M={M} N={N} K={K} group={group}")
     _, pk, sc = o.synth_weights(N, K, 55, group)
