@@ -193,6 +193,9 @@ def main() -> int:
     ap.add_argument("--only-dominant", action="store_true",
                     help="run only the dominant kernel's timing (gate_up, M=1): the workload of the committed "
                          "rocprofv3 kernel-trace and --pmc summaries")
+    ap.add_argument("--config", type=str, default=None,
+                    help="M,K,N: run only the timing of that one linear (graph of back-to-back launches over "
+                         "weight sets larger than the MALL); the workload of the per-regime rocprofv3 summaries")
     ap.add_argument("--copy-calibration", action="store_true",
                     help="run only a plain device copy of known size (256 MiB read + 256 MiB write, 20 times): "
                          "the scale for rocprofv3 FETCH_SIZE / WRITE_SIZE")
@@ -221,6 +224,14 @@ def main() -> int:
             dst.copy_(src)
         torch.cuda.synchronize()
         print(json.dumps({"copy_calibration": {"read_bytes": 4 * n, "write_bytes": 4 * n, "launches": 20}}), flush=True)
+        return 0
+
+    if args.config:
+        cM, cK, cN = (int(v) for v in args.config.split(","))
+        r = time_config(torch, w4a16, o, cM, cK, cN)
+        print(json.dumps({"M": cM, "K": cK, "N": cN, "bytes_per_launch": r["bytes"], "flops_per_launch": r["flops"],
+                          "avg_launch_us": round(r["us"], 3), "GBps": round(r["GBps"], 1),
+                          "TFLOPs": round(r["TFLOPs"], 2), "launches_per_replay": r["launches"]}), flush=True)
         return 0
 
     if args.only_dominant:

@@ -995,11 +995,15 @@ __global__ void __launch_bounds__(256) prefill_kernel(PrefillArgs a) {
     for (int i = 0; i < MB; ++i) xa[0][i] = *reinterpret_cast<const bf16x8*>(&xs[buf][32 * i + l32][32 * h]);
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
+      // A fragments of step j+1 go out before the MFMAs of step j; the scheduling
+      // barriers keep the compiler from sinking them next to their uses (it does
+      // not know the asm MFMAs' latency and would serialize load -> wait -> MFMA).
       if (j < 3) {
 #pragma unroll
         for (int i = 0; i < MB; ++i)
           xa[(j + 1) & 1][i] = *reinterpret_cast<const bf16x8*>(&xs[buf][32 * i + l32][32 * h + 8 * (j + 1)]);
       }
+      __builtin_amdgcn_sched_barrier(0);
       bf16x8 bb[TN];
 #pragma unroll
       for (int t = 0; t < TN; ++t) {
@@ -1010,6 +1014,7 @@ __global__ void __launch_bounds__(256) prefill_kernel(PrefillArgs a) {
       for (int i = 0; i < MB; ++i)
 #pragma unroll
         for (int t = 0; t < TN; ++t) mfma32_acc(acc[i][t], xa[j & 1][i], bb[t]);
+      __builtin_amdgcn_sched_barrier(0);
     }
   };
 
