@@ -1,0 +1,165 @@
+// w4lin_tool -- command-line front end of the C++ host mirror (w4lin.hpp).
+//
+//   w4lin_tool census <file.safetensors> [--expect N]
+//       one JSON line per packed linear, then a summary line; exit 1 on any failed
+//       check or when the count differs from N (328 for the 12B checkpoint).
+//   w4lin_tool layer12 <file.safetensors> <prefix> <j>
+//       the linears layer j of the 12B model consumes (g12.zig wiring), each checked.
+//   w4lin_tool linear <file.safetensors> <name> <M> <x.bin> <y.bin> [bf16|f32]
+//       y[M, n] = x[M, k] . toW()^T on the GPU; x.bin holds M*k bf16 values, y.bin
+//       receives M*n bf16 (default) or f32 values.
+//   w4lin_tool dequant <file.safetensors> <name> <w.bin>
+//       w[n, k] = toW() (bf16) on the GPU.
+#include <hip/hip_runtime.h>
+
+#include <cstdio>
+#include <cstdlib>
+#include <cstring>
+#include <fstream>
+#include <iostream>
+#include <string>
+#include <vector>
+
+#include "w4lin.hpp"
+
+namespace {
+
+int usage() {
+  std::fprintf(stderr,
+               "usage: w4lin_tool census <file> [--expect N]\n"
+               "       w4lin_tool layer12 <file> <prefix> <j>\n"
+               "       w4lin_tool linear <file> <name> <M> <x.bin> <y.bin> [bf16|f32]\n"
+               "       w4lin_tool dequant <file> <name> <w.bin>\n");
+  return 2;
+}
+
+std::vector<char> read_file(const std::string& path, size_t expect) {
+  std::ifstream f(path, std::ios::binary);
+  if (!f) throw std::runtime_error("cannot read " + path);
+  std::vector<char> b((std::istreambuf_iterator<char>(f)), std::istreambuf_iterator<char>());
+  if (b.size() != expect)
+    throw std::runtime_error(path + ": " + std::to_string(b.size()) + " bytes, expected " + std::to_string(expect));
+  return b;
+}
+
+void write_file(const std::string& path, const void* p, size_t n) {
+  std::ofstream f(path, std::ios::binary);
+  f.write(static_cast<const char*>(p), (std::streamsize)n);
+  if (!f) throw std::runtime_error("cannot write " + path);
+}
+
+void hip_ok(hipError_t e, const char* what) {
+  if (e != hipSuccess) throw std::runtime_error(std::string(what) + ": " + hipGetErrorString(e));
+}
+
+std::string json_escape(const std::string& s) {
+  std::string o;
+  for (char c : s) {
+    if (c == '"' || c == '\\') o.push_back('\\');
+    o.push_back(c);
+  }
+  return o;
+}
+
+int cmd_census(int argc, char** argv) {
+  if (argc < 3) return usage();
+  long expect = -1;
+  for (int i = 3; i + 1 < argc; ++i)
+    if (!std::strcmp(argv[i], "--expect")) expect = std::atol(argv[i + 1]);
+  w4::SafeTensorsFile f(argv[2]);
+  const w4::Census c = w4::census(f);
+  for (const auto& e : c.linears)
+    std::printf("{\"name\": \"%s\", \"n\": %lld, \"k\": %lld, \"group\": %d, \"weight_shape\": %s}\n",
+                json_escape(e.name).c_str(), (long long)e.n, (long long)e.k, e.group, e.has_shape ? "true" : "false");
+  std::printf("{\"linears\": %zu, \"errors\": [", c.linears.size());
+  for (size_t i = 0; i < c.errors.size(); ++i) std::printf("%s\"%s\"", i ? ", " : "", json_escape(c.errors[i]).c_str());
+  std::printf("]}\n");
+  if (!c.errors.empty()) return 1;
+  if (expect >= 0 && (long)c.linears.size() != expect) {
+    std::fprintf(stderr, "census: %zu linears, expected %ld\n", c.linears.size(), expect);
+    return 1;
+  }
+  return 0;
+}
+
+int cmd_layer12(int argc, char** argv) {
+  if (argc < 5) return usage();
+  w4::SafeTensorsFile f(argv[2]);
+  const w4::Census c = w4::census(f);
+  const int j = std::atoi(argv[4]);
+  int bad = 0;
+  for (const std::string& name : w4::g12_layer_linears(argv[3], j)) {
+    bool found = false;
+    for (const auto& e : c.linears)
+      if (e.name == name) {
+        std::printf("{\"name\": \"%s\", \"n\": %lld, \"k\": %lld}\n", json_escape(name).c_str(), (long long)e.n,
+                    (long long)e.k);
+        found = true;
+      }
+    if (!found) {
+      std::printf("{\"name\": \"%s\", \"missing\": true}\n", json_escape(name).c_str());
+      ++bad;
+    }
+  }
+  return bad ? 1 : 0;
+}
+
+int cmd_linear(int argc, char** argv) {
+  if (argc < 7) return usage();
+  const bool f32 = argc > 7 && !std::strcmp(argv[7], "f32");
+  const int64_t M = std::atoll(argv[4]);
+  w4::DeviceStore store(argv[2]);
+  const w4::W4Lin lin = w4::W4Lin::init(store, argv[3]);
+  const auto x = read_file(argv[5], (size_t)(M * lin.k * 2));
+  const size_t ybytes = (size_t)(M * lin.n * (f32 ? 4 : 2));
+  void *dx = nullptr, *dy = nullptr;
+  hip_ok(hipMalloc(&dx, std::max<size_t>(x.size(), 16)), "hipMalloc x");
+  hip_ok(hipMalloc(&dy, std::max<size_t>(ybytes, 16)), "hipMalloc y");
+  hip_ok(hipMemcpy(dx, x.data(), x.size(), hipMemcpyHostToDevice), "copy x");
+  if (f32) lin.linear(static_cast<const uint16_t*>(dx), static_cast<float*>(dy), M, nullptr);
+  else lin.linear(static_cast<const uint16_t*>(dx), static_cast<uint16_t*>(dy), M, nullptr);
+  std::vector<char> y(ybytes);
+  hip_ok(hipMemcpy(y.data(), dy, ybytes, hipMemcpyDeviceToHost), "copy y");
+  write_file(argv[6], y.data(), ybytes);
+  (void)hipFree(dx);
+  (void)hipFree(dy);
+  std::printf("{\"name\": \"%s\", \"M\": %lld, \"n\": %lld, \"k\": %lld, \"group\": %d, \"y\": \"%s\"}\n",
+              json_escape(argv[3]).c_str(), (long long)M, (long long)lin.n, (long long)lin.k, lin.group,
+              f32 ? "f32" : "bf16");
+  return 0;
+}
+
+int cmd_dequant(int argc, char** argv) {
+  if (argc < 5) return usage();
+  w4::DeviceStore store(argv[2]);
+  const w4::W4Lin lin = w4::W4Lin::init(store, argv[3]);
+  const size_t bytes = (size_t)(lin.n * lin.k * 2);
+  void* dw = nullptr;
+  hip_ok(hipMalloc(&dw, std::max<size_t>(bytes, 16)), "hipMalloc w");
+  lin.toW(static_cast<uint16_t*>(dw), nullptr);
+  std::vector<char> w(bytes);
+  hip_ok(hipMemcpy(w.data(), dw, bytes, hipMemcpyDeviceToHost), "copy w");
+  write_file(argv[4], w.data(), bytes);
+  (void)hipFree(dw);
+  return 0;
+}
+
+}  // namespace
+
+int main(int argc, char** argv) {
+  if (argc < 2) return usage();
+  try {
+    const std::string cmd = argv[1];
+    if (cmd == "census") return cmd_census(argc, argv);
+    if (cmd == "layer12") return cmd_layer12(argc, argv);
+    if (cmd == "linear") return cmd_linear(argc, argv);
+    if (cmd == "dequant") return cmd_dequant(argc, argv);
+    return usage();
+  } catch (const w4::Error& e) {
+    std::fprintf(stderr, "w4lin_tool: %s (status %d)\n", e.what(), e.status());
+    return 3;
+  } catch (const std::exception& e) {
+    std::fprintf(stderr, "w4lin_tool: %s\n", e.what());
+    return 3;
+  }
+}
