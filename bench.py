@@ -182,6 +182,45 @@ def cpu_baseline(budget_s: float = 15.0):
                       f"{med * 1e3:.1f} ms/step; os.cpu_count()={os.cpu_count()}; cpu={cpu_model}"}
 
 
+def time_gate_up(torch, w4a16, o, M, K, F):
+    """Average duration of one fused w4a16_gate_up_gelu launch (h bf16 [M, F]) against the
+    unfused composition (one linear over the concatenated [2F, K] weight, then torch's
+    gelu(approximate="tanh") * mul on the bf16 halves), both as HIP graphs over weight sets
+    larger than the MALL."""
+    wbytes = 2 * (F * K // 2 + F * K // 16)
+    nbytes = wbytes + 2 * M * K + 2 * M * F
+    nsets = max(2, -(-ROTATE_BYTES // wbytes))
+    sets = [make_set(torch, o, K, 2 * F, 7500 + i) for i in range(nsets)]
+    lins = [(w4a16.W4Lin(pk[:F], sc[:F]), w4a16.W4Lin(pk[F:], sc[F:])) for pk, sc in sets]
+    x = synth_x_dev(torch, o, M, K)
+    h = torch.empty((M, F), dtype=torch.bfloat16, device="cuda")
+    y = torch.empty((M, 2 * F), dtype=torch.bfloat16, device="cuda")
+    launches = nsets * max(1, -(-40 // nsets)) if M < 512 else nsets
+    reps = 5 if M < 512 else 2
+
+    def fused():
+        for i in range(launches):
+            g, u = lins[i % nsets]
+            w4a16.gate_up_gelu(x, g, u, out=h)
+
+    def unfused():
+        for i in range(launches):
+            pk, sc = sets[i % nsets]
+            w4a16.linear(x, pk, sc, out=y)
+            torch.mul(torch.nn.functional.gelu(y[:, :F], approximate="tanh"), y[:, F:], out=h)
+
+    out = {"M": M, "K": K, "F": F, "bytes": nbytes, "flops": 4 * M * F * K, "sets": nsets, "launches": launches}
+    for name, fn in (("fused", fused), ("unfused", unfused)):
+        g = graph_of(torch, fn)
+        out[name + "_us"] = time_graph(torch, g, reps) / (reps * launches) * 1e6
+        del g
+    del sets, lins
+    torch.cuda.empty_cache()
+    t = out["fused_us"] * 1e-6
+    out.update({"GBps": nbytes / t / 1e9, "TFLOPs": 4 * M * F * K / t / 1e12})
+    return out
+
+
 def main() -> int:
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -196,6 +235,9 @@ def main() -> int:
     ap.add_argument("--config", type=str, default=None,
                     help="M,K,N: run only the timing of that one linear (graph of back-to-back launches over "
                          "weight sets larger than the MALL); the workload of the per-regime rocprofv3 summaries")
+    ap.add_argument("--gate-up", type=str, default=None,
+                    help="M,K,F: time only the fused gate/up + gelu*mul call (w4a16_gate_up_gelu) against the "
+                         "unfused composition; the workload of the gate/up rocprofv3 summaries")
     ap.add_argument("--copy-calibration", action="store_true",
                     help="run only a plain device copy of known size (256 MiB read + 256 MiB write, 20 times): "
                          "the scale for rocprofv3 FETCH_SIZE / WRITE_SIZE")
@@ -232,6 +274,15 @@ def main() -> int:
         print(json.dumps({"M": cM, "K": cK, "N": cN, "bytes_per_launch": r["bytes"], "flops_per_launch": r["flops"],
                           "avg_launch_us": round(r["us"], 3), "GBps": round(r["GBps"], 1),
                           "TFLOPs": round(r["TFLOPs"], 2), "launches_per_replay": r["launches"]}), flush=True)
+        return 0
+
+    if args.gate_up:
+        gM, gK, gF = (int(v) for v in args.gate_up.split(","))
+        r = time_gate_up(torch, w4a16, o, gM, gK, gF)
+        print(json.dumps({"M": gM, "K": gK, "F": gF, "bytes_per_launch": r["bytes"], "flops_per_launch": r["flops"],
+                          "fused_us": round(r["fused_us"], 3), "unfused_us": round(r["unfused_us"], 3),
+                          "GBps": round(r["GBps"], 1), "TFLOPs": round(r["TFLOPs"], 2),
+                          "launches_per_replay": r["launches"]}), flush=True)
         return 0
 
     if args.only_dominant:

@@ -149,4 +149,73 @@ int w4a16_linear(const void* x, int32_t x_dtype, const int32_t* pk, const uint16
   return hip_status(w4l_linear(planes, nterms, pk, sc, y, y_f32, M, N, K, group, st), fn);
 }
 
+size_t w4a16_gate_up_workspace_size(int64_t M, int64_t F, int64_t K, int32_t x_dtype) {
+  if (M <= 0 || F <= 0 || K <= 0) return 0;
+  const size_t split = w4a16_workspace_size(M, F, K, x_dtype);
+  const int nterms = x_dtype == W4A16_DTYPE_F32 ? 3 : 1;
+  if (w4l_gate_up_fused(M, F, K, nterms)) return split;
+  return split + 2 * round_up((size_t)4 * (size_t)M * (size_t)F, 256);  // f32 g, then u
+}
+
+int w4a16_gate_up_gelu(const void* x, int32_t x_dtype, const int32_t* pk_gate, const uint16_t* sc_gate,
+                       const int32_t* pk_up, const uint16_t* sc_up, void* h, int32_t h_dtype, int64_t M,
+                       int64_t F, int64_t K, int32_t group, int32_t flags, void* workspace, size_t ws_bytes,
+                       void* stream) {
+  static const char* fn = "w4a16_gate_up_gelu";
+  clear_err();
+  int rc = check_dims(fn, M, F, K);
+  if (rc) return rc;
+  // the fused launch runs over 16 * ceil(F / 8) virtual rows
+  if (F > INT_MAX / 2 - 16) return fail(W4A16_EINVAL_SHAPE, "%s: F=%lld is too large", fn, (long long)F);
+  if ((rc = check_group(fn, K, group))) return rc;
+  if (x_dtype != W4A16_DTYPE_BF16 && x_dtype != W4A16_DTYPE_F32)
+    return fail(W4A16_EINVAL_ARG, "%s: unknown x_dtype %d", fn, (int)x_dtype);
+  if (h_dtype != W4A16_DTYPE_BF16 && h_dtype != W4A16_DTYPE_F32)
+    return fail(W4A16_EINVAL_ARG, "%s: unknown h_dtype %d", fn, (int)h_dtype);
+  if (flags & ~W4A16_GATE_UP_BF16_DOTS) return fail(W4A16_EINVAL_ARG, "%s: unknown flags 0x%x", fn, (unsigned)flags);
+  if (M == 0 || F == 0) return W4A16_OK;
+  if ((rc = check_ptr(h, "h", fn))) return rc;
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  const int h_f32 = h_dtype == W4A16_DTYPE_F32;
+  // K == 0: g = u = 0 and gelu(0) * 0 = 0
+  if (K == 0) return hip_status(w4l_fill_zero(h, M * F * (h_f32 ? 4 : 2), st), fn);
+  if ((rc = check_ptr(x, "x", fn)) || (rc = check_ptr(pk_gate, "pk_gate", fn)) ||
+      (rc = check_ptr(sc_gate, "sc_gate", fn)) || (rc = check_ptr(pk_up, "pk_up", fn)) ||
+      (rc = check_ptr(sc_up, "sc_up", fn)))
+    return rc;
+  const size_t need = w4a16_gate_up_workspace_size(M, F, K, x_dtype);
+  if (need) {
+    if (workspace == nullptr || ws_bytes < need)
+      return fail(W4A16_EWORKSPACE, "%s: this shape needs %zu bytes of workspace, got %zu", fn, need,
+                  workspace ? ws_bytes : (size_t)0);
+    if ((rc = check_ptr(workspace, "workspace", fn))) return rc;
+  } else if (workspace != nullptr && !aligned16(workspace)) {
+    return fail(W4A16_EINVAL_PTR, "%s: workspace is not 16-byte aligned", fn);
+  }
+
+  const uint16_t* planes = static_cast<const uint16_t*>(x);
+  int nterms = 1;
+  char* ws = static_cast<char*>(workspace);
+  if (x_dtype == W4A16_DTYPE_F32) {
+    uint16_t* split = reinterpret_cast<uint16_t*>(ws);
+    if ((rc = hip_status(w4l_split3(static_cast<const float*>(x), split, M * K, st), fn))) return rc;
+    planes = split;
+    nterms = 3;
+    ws += w4a16_workspace_size(M, F, K, x_dtype);
+  }
+  W4Pair pair;
+  pair.pk_up = pk_up;
+  pair.sc_up = sc_up;
+  pair.F = F;
+  pair.bf16_dots = (flags & W4A16_GATE_UP_BF16_DOTS) ? 1 : 0;
+  if (w4l_gate_up_fused(M, F, K, nterms))
+    return hip_status(w4l_gate_up(planes, nterms, pk_gate, sc_gate, pair, h, h_f32, M, K, group, st), fn);
+  // unfused route: g and u in f32 through the workspace, then the activation
+  float* g = reinterpret_cast<float*>(ws);
+  float* u = reinterpret_cast<float*>(ws + round_up((size_t)4 * (size_t)M * (size_t)F, 256));
+  if ((rc = hip_status(w4l_linear(planes, nterms, pk_gate, sc_gate, g, 1, M, F, K, group, st), fn))) return rc;
+  if ((rc = hip_status(w4l_linear(planes, nterms, pk_up, sc_up, u, 1, M, F, K, group, st), fn))) return rc;
+  return hip_status(w4l_gelu_mul(g, u, h, h_f32, pair.bf16_dots, M * F, st), fn);
+}
+
 }  // extern "C"

@@ -45,6 +45,75 @@ __device__ __forceinline__ uint32_t f32_to_bf16_rne(float f) {
   return ((u & 0x7fffffffu) > 0x7f800000u) ? 0x7fc0u : r;
 }
 
+// ---------------------------------------------------------------- gate/up pairs
+// Gemma's MLP front half (zml_runner/engine.zig:653): h = gelu(x . Wg^T) * (x . Wu^T).
+// The linear kernels run it as one launch over a virtual weight of 16 * ceil(F / 8)
+// rows in which every aligned 16-row tile holds 8 gate rows and the 8 matching up
+// rows: virtual row v is row ((v >> 4) << 3) | (v & 7) of gate (v & 8 == 0) or of
+// up (v & 8 != 0).  Each kernel's 16-row weight tile sits on 16 consecutive lanes
+// (lane & 15 == v & 15), so the up value of a gate row is one lane-xor-8 away and
+// the product is formed in registers before the only store.
+
+// Row pointers of virtual row v (clamped into range; rows past the end are
+// recomputed and not stored).  pair_f == 0: plain linear, row min(v, N - 1).
+__device__ __forceinline__ void weight_row(const uint32_t* pk, const uint16_t* sc, const uint32_t* pk2,
+                                           const uint16_t* sc2, int pair_f, int v, int N, int K,
+                                           int groups_per_row, const uint32_t*& pkrow,
+                                           const uint16_t*& scrow) {
+  int n = min(v, N - 1);
+  if (pair_f) {
+    n = min(((v >> 4) << 3) | (v & 7), pair_f - 1);
+    if (v & 8) {
+      pk = pk2;
+      sc = sc2;
+    }
+  }
+  pkrow = pk + (int64_t)n * (K >> 3);
+  scrow = sc + (int64_t)n * groups_per_row;
+}
+
+// gelu with the tanh approximation, as ZML's Tensor.gelu (gelu_pytorch_tanh):
+// 0.5 g (1 + tanh(z)), z = sqrt(2/pi) (g + 0.044715 g^3), in fp32.  Evaluated
+// through the identity 0.5 (1 + tanh(z)) = 1 / (1 + exp(-2 z)): no cancellation
+// where tanh(z) is near -1, and branch-free (the epilogues that call it are
+// fully unrolled over the accumulator registers).  exp(-2z) = 2^(-2z log2 e) on
+// v_exp_f32; overflow to +inf gives -0 for very negative g, as the tanh form.
+__device__ __forceinline__ float gelu_tanh(float g) {
+  const float z = 0.7978845608028654f * (g + 0.044715f * g * g * g);
+  const float e = __builtin_amdgcn_exp2f(-2.8853900817779268f * z);  // -2 log2(e) z
+  return g * __builtin_amdgcn_rcpf(1.0f + e);  // v_rcp_f32: 1 ulp
+}
+
+// Compile-time loop: f(integral_constant<int, I>) for I in [B, E).  Expands
+// fully whatever the unroller's thresholds, so register arrays indexed by I
+// stay in registers.
+template <int B, int E, class Fn>
+__device__ __forceinline__ void static_for(Fn&& f) {
+  if constexpr (B < E) {
+    f(std::integral_constant<int, B>{});
+    static_for<B + 1, E>(f);
+  }
+}
+
+// h = gelu(g) * u; with bf16_dots, g and u are first rounded to bf16 (the dot
+// outputs of dotPrec with fam = bf16, engine.zig:531).
+__device__ __forceinline__ void store_gelu_mul(void* y, int y_f32, int bf16_dots, int64_t idx, float g,
+                                               float u) {
+  if (bf16_dots) {
+    g = bf16_bits_to_f32(f32_to_bf16_rne(g));
+    u = bf16_bits_to_f32(f32_to_bf16_rne(u));
+  }
+  const float h = gelu_tanh(g) * u;
+  if (y_f32) reinterpret_cast<float*>(y)[idx] = h;
+  else reinterpret_cast<uint16_t*>(y)[idx] = (uint16_t)f32_to_bf16_rne(h);
+}
+
+// Value of lane (lane ^ 8): DPP row_ror:8 within each row of 16 lanes.  Every
+// lane of the row must be active.
+__device__ __forceinline__ float lane_xor8(float v) {
+  return __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), 0x128, 0xf, 0xf, false));
+}
+
 // ---------------------------------------------------------------- in-register dequant
 // 8 nibbles of one packed word -> 8 bf16 weights RNE(q * s) in column order,
 // laid out as one MFMA B operand (4 VGPRs, pairs (w0,w1) .. (w6,w7)).
@@ -340,6 +409,12 @@ struct GemvArgs {
   int groups_per_row;  // K / group
   int y_f32;
   int steps;           // ceil(K / GSTEP)
+  // gate/up pair mode (gemv_fast_kernel only): pk/sc are gate, pk2/sc2 up,
+  // pair_f = F real rows each (0 = plain linear), N = 16 * ceil(F / 8).
+  const uint32_t* pk2;
+  const uint16_t* sc2;
+  int pair_f;
+  int bf16_dots;
 };
 
 // NT: bf16 x planes (1, or 3 for f32 x).  KFULL: K % GSTEP == 0 (no partial
@@ -500,9 +575,9 @@ __global__ void __launch_bounds__(1024) gemv_fast_kernel(GemvArgs a) {
 #pragma unroll
   for (int tp = 0; tp < TPW; ++tp) {
     const int tile = min((int)blockIdx.x * TPW + tp, ntiles - 1);
-    const int nrow = min(tile * 16 + r, a.N - 1);
-    const uint32_t* pkrow = a.pk + (int64_t)nrow * (a.K >> 3);
-    const uint16_t* scrow = a.sc + (int64_t)nrow * a.groups_per_row;
+    const uint32_t* pkrow;
+    const uint16_t* scrow;
+    weight_row(a.pk, a.sc, a.pk2, a.sc2, a.pair_f, tile * 16 + r, a.N, a.K, a.groups_per_row, pkrow, scrow);
 #pragma unroll
     for (int i = 0; i < NST; ++i) {
       const int g0 = ((s0 + i) * 4 + c) * VPL;
@@ -563,7 +638,18 @@ __global__ void __launch_bounds__(1024) gemv_fast_kernel(GemvArgs a) {
   if ((int)threadIdx.x < 16 * 4 * TPW) {
     const int tp = threadIdx.x >> 6, m = (threadIdx.x >> 4) & 3, rr = threadIdx.x & 15;
     const int n = ((int)blockIdx.x * TPW + tp) * 16 + rr;
-    if (m < a.M && n < a.N) {
+    if (a.pair_f) {
+      // gate row rr < 8 of the tile and its up row rr + 8
+      const int f = (((int)blockIdx.x * TPW + tp) << 3) + rr;
+      if (rr < 8 && m < a.M && f < a.pair_f) {
+        float g = 0.f, u = 0.f;
+        for (int w = 0; w < nwaves; ++w) {
+          g += red[((tp * nwaves + w) * 4 + m) * 16 + rr];
+          u += red[((tp * nwaves + w) * 4 + m) * 16 + rr + 8];
+        }
+        store_gelu_mul(a.y, a.y_f32, a.bf16_dots, (int64_t)m * a.pair_f + f, g, u);
+      }
+    } else if (m < a.M && n < a.N) {
       float v = 0.f;
       for (int w = 0; w < nwaves; ++w) v += red[((tp * nwaves + w) * 4 + m) * 16 + rr];
       if (a.y_f32) reinterpret_cast<float*>(a.y)[(int64_t)m * a.N + n] = v;
@@ -733,6 +819,11 @@ struct SkinnyArgs {
   int groups_per_row;  // K / group
   int y_f32;
   int nk;              // K / 256
+  // gate/up pair mode, as GemvArgs
+  const uint32_t* pk2;
+  const uint16_t* sc2;
+  int pair_f;
+  int bf16_dots;
 };
 
 constexpr int SK_P = 4;  // weight prefetch depth (chunks); even, for the two-slot x ring
@@ -746,9 +837,10 @@ __global__ void __launch_bounds__(256) skinny_kernel(SkinnyArgs a) {
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int r = lane & 15, c = lane >> 4;
   const int m0 = blockIdx.y * (16 * MT);
-  const int n = min((int)blockIdx.x * 64 + 16 * wave + r, a.N - 1);
-  const uint32_t* pkrow = a.pk + (int64_t)n * (a.K >> 3);
-  const uint16_t* scrow = a.sc + (int64_t)n * a.groups_per_row;
+  const uint32_t* pkrow;
+  const uint16_t* scrow;
+  weight_row(a.pk, a.sc, a.pk2, a.sc2, a.pair_f, (int)blockIdx.x * 64 + 16 * wave + r, a.N, a.K,
+             a.groups_per_row, pkrow, scrow);
 
   // weight ring: chunk k -> slot k % P; lane (r, c) holds the 32-column chunks
   // 8k + 2c and 8k + 2c + 1 of its row (two 16-byte vectors) and their scales.
@@ -859,7 +951,23 @@ __global__ void __launch_bounds__(256) skinny_kernel(SkinnyArgs a) {
 
   // D layout: lane (n = r, c) holds D[m = 4c + i][n]
   const int nout = (int)blockIdx.x * 64 + 16 * wave + r;
-  if (nout < a.N) {
+  if (a.pair_f) {
+    // Lanes r and r ^ 8 hold gate and up of row f for the same m; per pair of
+    // rows m, m + 1 the gate lane finishes m and the up lane m + 1 (all lanes
+    // active here).
+    const int f = ((nout >> 4) << 3) | (r & 7);
+    const int up = (r >> 3) & 1;
+#pragma unroll
+    for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+      for (int i = 0; i < 4; i += 2) {
+        const float p0 = lane_xor8(acc[mt][i]), p1 = lane_xor8(acc[mt][i + 1]);
+        const float g = up ? p1 : acc[mt][i];
+        const float u = up ? acc[mt][i + 1] : p0;
+        const int m = m0 + 16 * mt + 4 * c + i + up;
+        if (f < a.pair_f && m < a.M) store_gelu_mul(a.y, a.y_f32, a.bf16_dots, (int64_t)m * a.pair_f + f, g, u);
+      }
+  } else if (nout < a.N) {
 #pragma unroll
     for (int mt = 0; mt < MT; ++mt)
 #pragma unroll
@@ -905,6 +1013,11 @@ struct PrefillArgs {
   int y_f32;
   int ns;    // K / 64
   int mblk;  // ceil(M / 256)
+  // gate/up pair mode, as GemvArgs
+  const uint32_t* pk2;
+  const uint16_t* sc2;
+  int pair_f;
+  int bf16_dots;
 };
 
 template <int TN, int P, bool G32>
@@ -923,11 +1036,9 @@ __global__ void __launch_bounds__(256) prefill_kernel(PrefillArgs a) {
   const uint32_t* pkrow[TN];
   const uint16_t* scrow[TN];
 #pragma unroll
-  for (int t = 0; t < TN; ++t) {
-    const int n = min(nw0 + 32 * t + l32, a.N - 1);
-    pkrow[t] = a.pk + (int64_t)n * (a.K >> 3);
-    scrow[t] = a.sc + (int64_t)n * a.groups_per_row;
-  }
+  for (int t = 0; t < TN; ++t)
+    weight_row(a.pk, a.sc, a.pk2, a.sc2, a.pair_f, nw0 + 32 * t + l32, a.N, a.K, a.groups_per_row, pkrow[t],
+               scrow[t]);
   uint4 wv[P][TN];
   uint32_t sv[P][TN];
   auto wload = [&](auto slot_c, int s) __attribute__((always_inline)) {
@@ -1041,24 +1152,51 @@ __global__ void __launch_bounds__(256) prefill_kernel(PrefillArgs a) {
   // the last MFMAs must finish before their AGPRs are read (16-pass MFMA: >= 18 wait states)
   asm volatile("s_nop 7\n\ts_nop 7\n\ts_nop 7\n\ts_nop 7" ::: "memory");
 
-#pragma unroll
-  for (int t = 0; t < TN; ++t) {
+  static_for<0, TN>([&](auto t_c) __attribute__((always_inline)) {
+    constexpr int t = decltype(t_c)::value;
     const int n = nw0 + 32 * t + l32;
-    if (n < a.N) {
-#pragma unroll
-      for (int i = 0; i < MB; ++i) {
-        const floatx16 v = acc[i][t];
+    if (a.pair_f) {
+      // Lanes l and l ^ 8 hold gate and up of row f for the same m.  Per pair of
+      // values e, e + 1 (rows m, m + 1) the gate lane finishes row m and the up
+      // lane row m + 1, so each lane evaluates one activation per pair (all
+      // lanes active here).
+      const int f = ((n >> 4) << 3) | (l32 & 7);
+      const int up = (l32 >> 3) & 1;
+      static_for<0, MB>([&](auto i_c) __attribute__((always_inline)) {
+        constexpr int i = decltype(i_c)::value;
+        static_for<0, 8>([&](auto e_c) __attribute__((always_inline)) {
+          constexpr int e = 2 * decltype(e_c)::value;
+          const float p0 = lane_xor8(acc[i][t][e]), p1 = lane_xor8(acc[i][t][e + 1]);
+          const float g = up ? p1 : acc[i][t][e];
+          const float u = up ? acc[i][t][e + 1] : p0;
+          const int m = m0 + 32 * i + 8 * (e >> 2) + 4 * h + (e & 3) + up;
+          if (f < a.pair_f && m < a.M) store_gelu_mul(a.y, a.y_f32, a.bf16_dots, (int64_t)m * a.pair_f + f, g, u);
+        });
+      });
+    } else if (n < a.N) {
+      static_for<0, MB>([&](auto i_c) __attribute__((always_inline)) {
+        constexpr int i = decltype(i_c)::value;
 #pragma unroll
         for (int e = 0; e < 16; ++e) {
           const int m = m0 + 32 * i + 8 * (e >> 2) + 4 * h + (e & 3);
           if (m < a.M) {
-            if (a.y_f32) reinterpret_cast<float*>(a.y)[(int64_t)m * a.N + n] = v[e];
-            else reinterpret_cast<uint16_t*>(a.y)[(int64_t)m * a.N + n] = (uint16_t)f32_to_bf16_rne(v[e]);
+            const float v = acc[i][t][e];
+            if (a.y_f32) reinterpret_cast<float*>(a.y)[(int64_t)m * a.N + n] = v;
+            else reinterpret_cast<uint16_t*>(a.y)[(int64_t)m * a.N + n] = (uint16_t)f32_to_bf16_rne(v);
           }
         }
-      }
+      });
     }
-  }
+  });
+}
+
+// h = gelu(g) * u elementwise over f32 g, u: the combine step of the unfused
+// gate/up route (shapes no pair-mode kernel takes).
+__global__ void __launch_bounds__(256) gelu_mul_kernel(const float* __restrict__ g, const float* __restrict__ u,
+                                                       void* h, int h_f32, int bf16_dots, int64_t n) {
+  const int64_t stride = (int64_t)gridDim.x * blockDim.x;
+  for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += stride)
+    store_gelu_mul(h, h_f32, bf16_dots, i, g[i], u[i]);
 }
 
 // K == 0: y = 0 (a kernel rather than a memset, so callers may capture it in a graph).
@@ -1203,11 +1341,12 @@ bool w4l_gemv_stream_plan(int64_t M, int64_t N, int64_t K, int nterms, int* w_ou
 
 hipError_t w4l_gemv(const uint16_t* x_planes, int nterms, const int32_t* pk, const uint16_t* sc,
                     void* y, int y_f32, int64_t M, int64_t N, int64_t K, int32_t group,
-                    hipStream_t st) {
-  if (getenv("W4A16_GEMV_STREAM")) {
+                    hipStream_t st, const W4Pair* pair) {
+  if (pair) N = 16 * ((pair->F + 7) / 8);
+  if (!pair && getenv("W4A16_GEMV_STREAM")) {
     int w, nst, cpw, xpt;
     if (w4l_gemv_stream_plan(M, N, K, nterms, &w, &nst, &cpw, &xpt)) {
-      w4k::GemvArgs a;
+      w4k::GemvArgs a{};
       a.x = x_planes;
       a.pk = reinterpret_cast<const uint32_t*>(pk);
       a.sc = sc;
@@ -1253,7 +1392,7 @@ hipError_t w4l_gemv(const uint16_t* x_planes, int nterms, const int32_t* pk, con
   {
     int nst, waves, xpt, tpw;
     if (w4l_gemv_fast_plan(M, N, K, nterms, &nst, &waves, &xpt, &tpw)) {
-      w4k::GemvArgs a;
+      w4k::GemvArgs a{};
       a.x = x_planes;
       a.pk = reinterpret_cast<const uint32_t*>(pk);
       a.sc = sc;
@@ -1265,6 +1404,12 @@ hipError_t w4l_gemv(const uint16_t* x_planes, int nterms, const int32_t* pk, con
       a.groups_per_row = (int)(K / group);
       a.y_f32 = y_f32;
       a.steps = (int)(K / w4k::GSTEP);
+      if (pair) {
+        a.pk2 = reinterpret_cast<const uint32_t*>(pair->pk_up);
+        a.sc2 = pair->sc_up;
+        a.pair_f = (int)pair->F;
+        a.bf16_dots = pair->bf16_dots;
+      }
       const int64_t tiles = (N + 15) / 16;
       const size_t lds = (size_t)nterms * M * K * 2 + (size_t)tpw * waves * 4 * 16 * 4;
       const dim3 grid((unsigned)((tiles + tpw - 1) / tpw)), block(64 * waves);
@@ -1303,7 +1448,8 @@ hipError_t w4l_gemv(const uint16_t* x_planes, int nterms, const int32_t* pk, con
       return hipGetLastError();
     }
   }
-  w4k::GemvArgs a;
+  if (pair) return hipErrorInvalidValue;
+  w4k::GemvArgs a{};
   a.x = x_planes;
   a.pk = reinterpret_cast<const uint32_t*>(pk);
   a.sc = sc;
@@ -1355,8 +1501,15 @@ bool w4l_skinny_ok(int64_t M, int64_t K, int nterms) {
 }
 
 hipError_t w4l_skinny(const uint16_t* x, const int32_t* pk, const uint16_t* sc, void* y, int y_f32,
-                      int64_t M, int64_t N, int64_t K, int32_t group, hipStream_t st) {
-  w4k::SkinnyArgs a;
+                      int64_t M, int64_t N, int64_t K, int32_t group, hipStream_t st, const W4Pair* pair) {
+  w4k::SkinnyArgs a{};
+  if (pair) {
+    N = 16 * ((pair->F + 7) / 8);
+    a.pk2 = reinterpret_cast<const uint32_t*>(pair->pk_up);
+    a.sc2 = pair->sc_up;
+    a.pair_f = (int)pair->F;
+    a.bf16_dots = pair->bf16_dots;
+  }
   a.x = x;
   a.pk = reinterpret_cast<const uint32_t*>(pk);
   a.sc = sc;
@@ -1388,8 +1541,15 @@ bool w4l_prefill_ok(int64_t M, int64_t K, int nterms) {
 }
 
 hipError_t w4l_prefill(const uint16_t* x, const int32_t* pk, const uint16_t* sc, void* y, int y_f32,
-                       int64_t M, int64_t N, int64_t K, int32_t group, hipStream_t st) {
-  w4k::PrefillArgs a;
+                       int64_t M, int64_t N, int64_t K, int32_t group, hipStream_t st, const W4Pair* pair) {
+  w4k::PrefillArgs a{};
+  if (pair) {
+    N = 16 * ((pair->F + 7) / 8);
+    a.pk2 = reinterpret_cast<const uint32_t*>(pair->pk_up);
+    a.sc2 = pair->sc_up;
+    a.pair_f = (int)pair->F;
+    a.bf16_dots = pair->bf16_dots;
+  }
   a.x = x;
   a.pk = reinterpret_cast<const uint32_t*>(pk);
   a.sc = sc;
@@ -1424,7 +1584,7 @@ hipError_t w4l_linear(const uint16_t* x_planes, int nterms, const int32_t* pk, c
   if (w4l_prefill_ok(M, K, nterms)) return w4l_prefill(x_planes, pk, sc, y, y_f32, M, N, K, group, st);
   if (w4l_skinny_ok(M, K, nterms)) return w4l_skinny(x_planes, pk, sc, y, y_f32, M, N, K, group, st);
   const W4Plan p = w4l_plan(M, N, K, nterms);
-  w4k::LinearArgs a;
+  w4k::LinearArgs a{};
   a.x = x_planes;
   a.pk = reinterpret_cast<const uint32_t*>(pk);
   a.sc = sc;
@@ -1457,5 +1617,44 @@ hipError_t w4l_linear(const uint16_t* x_planes, int nterms, const int32_t* pk, c
     }
   }
 #undef W4_LAUNCH
+  return hipGetLastError();
+}
+
+namespace {
+enum PairRoute { PAIR_NONE, PAIR_GEMV, PAIR_PREFILL, PAIR_SKINNY };
+
+// Kernel of the fused gate/up launch, in the order of w4l_linear; the skinny
+// kernel also takes decode shapes the straight-line GEMV plan cannot hold (its
+// x rows past M repeat row M - 1 and are not stored).
+PairRoute pair_route(int64_t M, int64_t F, int64_t K, int nterms) {
+  int nst, waves, xpt, tpw;
+  if (w4l_gemv_ok(M, K, nterms) && w4l_gemv_fast_plan(M, 16 * ((F + 7) / 8), K, nterms, &nst, &waves, &xpt, &tpw))
+    return PAIR_GEMV;
+  if (w4l_prefill_ok(M, K, nterms)) return PAIR_PREFILL;
+  if (nterms == 1 && K % 256 == 0) return PAIR_SKINNY;
+  return PAIR_NONE;
+}
+}  // namespace
+
+bool w4l_gate_up_fused(int64_t M, int64_t F, int64_t K, int nterms) {
+  return pair_route(M, F, K, nterms) != PAIR_NONE;
+}
+
+hipError_t w4l_gate_up(const uint16_t* x_planes, int nterms, const int32_t* pk_gate, const uint16_t* sc_gate,
+                       const W4Pair& pair, void* h, int h_f32, int64_t M, int64_t K, int32_t group,
+                       hipStream_t st) {
+  switch (pair_route(M, pair.F, K, nterms)) {
+    case PAIR_GEMV: return w4l_gemv(x_planes, nterms, pk_gate, sc_gate, h, h_f32, M, 0, K, group, st, &pair);
+    case PAIR_PREFILL: return w4l_prefill(x_planes, pk_gate, sc_gate, h, h_f32, M, 0, K, group, st, &pair);
+    case PAIR_SKINNY: return w4l_skinny(x_planes, pk_gate, sc_gate, h, h_f32, M, 0, K, group, st, &pair);
+    default: return hipErrorInvalidValue;
+  }
+}
+
+hipError_t w4l_gelu_mul(const float* g, const float* u, void* h, int h_f32, int bf16_dots, int64_t n,
+                        hipStream_t st) {
+  const int block = 256;
+  hipLaunchKernelGGL(w4k::gelu_mul_kernel, dim3(grid_for(n, block)), dim3(block), 0, st, g, u, h, h_f32, bf16_dots,
+                     n);
   return hipGetLastError();
 }

@@ -18,24 +18,49 @@ struct W4Plan {
 
 W4Plan w4l_plan(int64_t M, int64_t N, int64_t K, int nterms);
 
+// Gate/up pair of the fused MLP front half (engine.zig:653): the launch's pk/sc
+// are the gate weight, these the up weight, both [F, K]; the output is
+// h[M, F] = gelu_tanh(g) * u.  Kernels that take one run over 16 * ceil(F / 8)
+// virtual rows (8 gate rows, then the 8 matching up rows, per 16-row tile).
+struct W4Pair {
+  const int32_t* pk_up;
+  const uint16_t* sc_up;
+  int64_t F;
+  int bf16_dots;  // round g and u to bf16 before gelu
+};
+
 // Decode GEMV path (M <= 4, x planes fit in 64 KiB of LDS).
 bool w4l_gemv_ok(int64_t M, int64_t K, int nterms);
 int w4l_gemv_waves(int64_t N, int64_t K);
 bool w4l_gemv_stream_plan(int64_t M, int64_t N, int64_t K, int nterms, int* w, int* nst, int* cpw, int* xpt);
 bool w4l_gemv_fast_plan(int64_t M, int64_t N, int64_t K, int nterms, int* nst, int* waves, int* xpt, int* tpw);
+// With a pair, only the straight-line plan is used (hipErrorInvalidValue when
+// w4l_gemv_fast_plan fails) and N is ignored.
 hipError_t w4l_gemv(const uint16_t* x_planes, int nterms, const int32_t* pk, const uint16_t* sc,
                     void* y, int y_f32, int64_t M, int64_t N, int64_t K, int32_t group,
-                    hipStream_t st);
+                    hipStream_t st, const W4Pair* pair = nullptr);
 
 // Skinny / prefill path (M > 4, bf16 x, K % 256 == 0).
 bool w4l_skinny_ok(int64_t M, int64_t K, int nterms);
 hipError_t w4l_skinny(const uint16_t* x, const int32_t* pk, const uint16_t* sc, void* y, int y_f32,
-                      int64_t M, int64_t N, int64_t K, int32_t group, hipStream_t st);
+                      int64_t M, int64_t N, int64_t K, int32_t group, hipStream_t st,
+                      const W4Pair* pair = nullptr);
 
 // Prefill path (M > 64, bf16 x, K % 64 == 0).
 bool w4l_prefill_ok(int64_t M, int64_t K, int nterms);
 hipError_t w4l_prefill(const uint16_t* x, const int32_t* pk, const uint16_t* sc, void* y, int y_f32,
-                       int64_t M, int64_t N, int64_t K, int32_t group, hipStream_t st);
+                       int64_t M, int64_t N, int64_t K, int32_t group, hipStream_t st,
+                       const W4Pair* pair = nullptr);
+
+// Fused gate/up + gelu * mul: true when one of the three kernels above takes
+// (M, F, K, nterms) in pair mode; w4l_gate_up launches it.  Otherwise the
+// caller composes two w4l_linear calls into f32 g, u and w4l_gelu_mul.
+bool w4l_gate_up_fused(int64_t M, int64_t F, int64_t K, int nterms);
+hipError_t w4l_gate_up(const uint16_t* x_planes, int nterms, const int32_t* pk_gate, const uint16_t* sc_gate,
+                       const W4Pair& pair, void* h, int h_f32, int64_t M, int64_t K, int32_t group,
+                       hipStream_t st);
+hipError_t w4l_gelu_mul(const float* g, const float* u, void* h, int h_f32, int bf16_dots, int64_t n,
+                        hipStream_t st);
 
 hipError_t w4l_unpack(const int32_t* pk, int8_t* q, int64_t nwords, hipStream_t st);
 hipError_t w4l_dequant(const int32_t* pk, const uint16_t* sc, uint16_t* w, int64_t N, int64_t K,

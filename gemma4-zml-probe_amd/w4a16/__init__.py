@@ -10,6 +10,8 @@ Host-side mirror of the reference's W4 brick interface
                                          .toW() dequantizes; .linear(x) is the fused call
   linear(x, pk, sc)       G3.forward, zml_runner/gemma4_w4gate.zig:288-292:
                           y = x . dequantW4(pk, sc)^T with fp32 accumulation
+  gate_up_gelu(x, gate, up)  the MLP front half, zml_runner/engine.zig:653:
+                          h = gelu_tanh(x . Wg^T) * (x . Wu^T) in one call
 
 Tensors are torch tensors on the GPU; torch is only the device-memory and
 stream plumbing.  Every call goes through libw4a16.so on the current torch
@@ -36,7 +38,9 @@ GROUP = 32
 
 # Every symbol include/w4a16.h declares.
 EXPORTS = ("w4a16_version", "w4a16_last_error", "w4a16_unpack", "w4a16_dequant",
-           "w4a16_workspace_size", "w4a16_linear")
+           "w4a16_workspace_size", "w4a16_linear", "w4a16_gate_up_workspace_size",
+           "w4a16_gate_up_gelu")
+GATE_UP_BF16_DOTS = 1
 
 
 class W4A16Error(RuntimeError):
@@ -74,6 +78,11 @@ def lib() -> ctypes.CDLL:
         L.w4a16_workspace_size.restype = ctypes.c_size_t
         L.w4a16_linear.argtypes = [P, I32, P, P, P, I32, I64, I64, I64, I32, I32, P, ctypes.c_size_t, P]
         L.w4a16_linear.restype = ctypes.c_int
+        L.w4a16_gate_up_workspace_size.argtypes = [I64, I64, I64, I32]
+        L.w4a16_gate_up_workspace_size.restype = ctypes.c_size_t
+        L.w4a16_gate_up_gelu.argtypes = [P, I32, P, P, P, P, P, I32, I64, I64, I64, I32, I32, P,
+                                         ctypes.c_size_t, P]
+        L.w4a16_gate_up_gelu.restype = ctypes.c_int
         _lib = L
     return _lib
 
@@ -89,6 +98,10 @@ def version() -> int:
 
 def workspace_size(M: int, N: int, K: int, x_dtype: int = DTYPE_BF16) -> int:
     return int(lib().w4a16_workspace_size(M, N, K, x_dtype))
+
+
+def gate_up_workspace_size(M: int, F: int, K: int, x_dtype: int = DTYPE_BF16) -> int:
+    return int(lib().w4a16_gate_up_workspace_size(M, F, K, x_dtype))
 
 
 # ------------------------------------------------------------ torch-facing API
@@ -182,6 +195,63 @@ def linear(x, pk, sc, out_dtype=None, group: int = GROUP, out=None, workspace=No
         ws_ptr, ws_bytes = workspace.data_ptr(), workspace.numel() * workspace.element_size()
     check(lib().w4a16_linear(x.data_ptr(), x_dtype, pk.data_ptr(), sc.data_ptr(), out.data_ptr(),
                              y_dtype, M, N, K, group, 0, ws_ptr, ws_bytes, _stream_ptr(x)))
+    return out
+
+
+def gate_up_gelu(x, gate: "W4Lin", up: "W4Lin", out_dtype=None, bf16_dots: bool = False, out=None,
+                 workspace=None):
+    """h[..., F] = gelu_tanh(x . gate.toW()^T) * (x . up.toW()^T) in one call: the front half
+    of the MLP, engine.zig:653 (``dotPrec(xff, gate_proj).gelu().mul(dotPrec(xff, up_proj))``).
+
+    gelu_tanh is ZML's Tensor.gelu (gelu_pytorch_tanh).  x bf16 or f32 [..., K]; out_dtype
+    bf16 (default for bf16 x) or f32 (default for f32 x).  bf16_dots rounds both dot
+    outputs to bf16 before the activation (dotPrec with fam = bf16).  Shapes no fused
+    kernel takes need workspace (allocated here when not given)."""
+    torch = _torch()
+    _dev_check(x, gate.pk, gate.sc, up.pk, up.sc)
+    if x.dtype not in (torch.bfloat16, torch.float32):
+        raise W4A16Error(EINVAL_ARG, "x must be bf16 or f32")
+    if gate.group != up.group:
+        raise W4A16Error(EINVAL_ARG, f"gate group {gate.group} != up group {up.group}")
+    for w in (gate, up):
+        if w.pk.dtype != torch.int32 or w.sc.dtype != torch.bfloat16 or w.pk.dim() != 2 or w.sc.dim() != 2:
+            raise W4A16Error(EINVAL_ARG, "pk must be int32 [F, K/8] and sc bf16 [F, K/group]")
+    F, K = gate.out_features, gate.in_features
+    if (up.out_features, up.in_features) != (F, K):
+        raise W4A16Error(EINVAL_SHAPE, f"up [{up.out_features}, {up.in_features}] != gate [{F}, {K}]")
+    for w in (gate, up):
+        if w.sc.shape[0] != F or w.sc.shape[1] * w.group != K:
+            raise W4A16Error(EINVAL_SHAPE, f"sc shape {tuple(w.sc.shape)} does not match [{F}, {K}] / {w.group}")
+    if x.shape[-1] != K:
+        raise W4A16Error(EINVAL_SHAPE, f"x last dim {x.shape[-1]} != K {K}")
+    lead = tuple(x.shape[:-1])
+    M = 1
+    for d in lead:
+        M *= d
+    x_dtype = DTYPE_BF16 if x.dtype == torch.bfloat16 else DTYPE_F32
+    if out is not None:
+        if out_dtype is not None and out_dtype != out.dtype:
+            raise W4A16Error(EINVAL_ARG, f"out_dtype {out_dtype} != out.dtype {out.dtype}")
+        out_dtype = out.dtype
+        _dev_check(out)
+        if out.numel() != M * F or out.shape[-1] != F:
+            raise W4A16Error(EINVAL_SHAPE, f"out shape {tuple(out.shape)} != {lead + (F,)}")
+    elif out_dtype is None:
+        out_dtype = x.dtype
+    if out_dtype not in (torch.bfloat16, torch.float32):
+        raise W4A16Error(EINVAL_ARG, "output must be bf16 or f32")
+    h_dtype = DTYPE_BF16 if out_dtype == torch.bfloat16 else DTYPE_F32
+    if out is None:
+        out = torch.empty(lead + (F,), dtype=out_dtype, device=x.device)
+    ws_need = gate_up_workspace_size(M, F, K, x_dtype)
+    ws_ptr, ws_bytes = None, 0
+    if ws_need:
+        if workspace is None:
+            workspace = torch.empty(ws_need, dtype=torch.uint8, device=x.device)
+        ws_ptr, ws_bytes = workspace.data_ptr(), workspace.numel() * workspace.element_size()
+    check(lib().w4a16_gate_up_gelu(x.data_ptr(), x_dtype, gate.pk.data_ptr(), gate.sc.data_ptr(), up.pk.data_ptr(),
+                                   up.sc.data_ptr(), out.data_ptr(), h_dtype, M, F, K, gate.group,
+                                   GATE_UP_BF16_DOTS if bf16_dots else 0, ws_ptr, ws_bytes, _stream_ptr(x)))
     return out
 
 

@@ -116,6 +116,51 @@ int w4a16_linear(const void *x, int32_t x_dtype,
                  int64_t M, int64_t N, int64_t K, int32_t group,
                  int32_t flags, void *workspace, size_t ws_bytes, void *stream);
 
+/* Flags of w4a16_gate_up_gelu. */
+enum {
+    /* g and u rounded to bf16 before the activation: the dot outputs of dotPrec
+     * with fam = bf16 (engine.zig:531, a.convert(bf16).dot(..).convert(compute)). */
+    W4A16_GATE_UP_BF16_DOTS = 1
+};
+
+/*
+ * Bytes of device workspace w4a16_gate_up_gelu needs for (M, F, K, x_dtype):
+ * the f32-activation split of w4a16_workspace_size, plus 2 * 4 * M * F bytes for
+ * f32 g and u on shapes that no fused kernel takes (then g and u make a round
+ * trip through the workspace).  The second part is 0 when a fused kernel
+ * takes the shape: bf16 x with K % 256 == 0 (any M) or with M > 64 and
+ * K % 64 == 0 (every Gemma gate/up shape: K = 1536 or 3840); f32 x in the
+ * decode GEMV (M <= 4, K % 256 == 0, within its LDS and register limits).
+ */
+size_t w4a16_gate_up_workspace_size(int64_t M, int64_t F, int64_t K, int32_t x_dtype);
+
+/*
+ * The front half of Gemma's MLP at engine.zig:653, both W4 linears and the
+ * activation in one call:
+ *     h[M, F] = gelu(x . Wg^T) * (x . Wu^T),
+ *     Wg = dequantW4(pk_gate, sc_gate), Wu = dequantW4(pk_up, sc_up), both [F, K],
+ *     gelu(g) = 0.5 g (1 + tanh(sqrt(2/pi) (g + 0.044715 g^3)))  (ZML Tensor.gelu,
+ *     the gelu_pytorch_tanh of the checkpoint config).
+ * Replaces "dotPrec(xff, gate_proj).gelu().mul(dotPrec(xff, up_proj))"; h then
+ * feeds down_proj through w4a16_linear.  g and u are exactly the two results
+ * w4a16_linear would produce in fp32 (same rounding of the weights, fp32
+ * accumulate); the activation and the product are evaluated in fp32.  On the
+ * fused shapes g and u never leave the registers: one launch reads x, both
+ * weights and writes h.
+ *   x_dtype   as w4a16_linear.
+ *   h_dtype   W4A16_DTYPE_F32 (compute = f32) or W4A16_DTYPE_BF16 (h rounded
+ *             once to nearest even).
+ *   flags     0 or W4A16_GATE_UP_BF16_DOTS.
+ *   group     shared by both weights.
+ *   workspace / ws_bytes  at least w4a16_gate_up_workspace_size(M, F, K, x_dtype).
+ */
+int w4a16_gate_up_gelu(const void *x, int32_t x_dtype,
+                       const int32_t *pk_gate, const uint16_t *sc_gate,
+                       const int32_t *pk_up, const uint16_t *sc_up,
+                       void *h, int32_t h_dtype,
+                       int64_t M, int64_t F, int64_t K, int32_t group,
+                       int32_t flags, void *workspace, size_t ws_bytes, void *stream);
+
 #ifdef __cplusplus
 }
 #endif

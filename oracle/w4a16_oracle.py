@@ -14,10 +14,22 @@ Reference functions restated (file:line in TheCause/gemma4-zml-probe):
            scripts/63_u_dequant_export.py:83-89
   linear   G3.forward, zml_runner/gemma4_w4gate.zig:288-292;
            scripts/58_w4_gemm_oracle.py:29 (x.f32 @ w.f32.T)
+  gelu_tanh     ZML Tensor.gelu = gelu_pytorch_tanh, docs/ROADMAP_to_full_forward.md:30
+                (ZML itself is a dependency that is not vendored in the reference)
+  gate_up_gelu  the MLP front half, zml_runner/engine.zig:653:
+                dot(xff, gate).gelu().mul(dot(xff, up)), gating gelu(gate) * up
+                (PLANNING.md:345), dots through dotPrec (engine.zig:530-533)
+Pins of the last two (tests/test_oracle.py): gelu_tanh against torch's independent
+gelu(approximate="tanh") in float64, against the defining tanh formula in 400-digit
+decimal arithmetic on the negative tail (where float tanh forms cancel), the odd-part
+identity gelu(x) - gelu(-x) = x, the limits and the closed-form values at 0 and 1;
+gate_up_gelu against a torch-only composition (bf16 dequant, float64 matmul, torch
+gelu) with planted mistakes (gelu(gate * up), gelu(up) * gate) that the check sees.
 """
 from __future__ import annotations
 
 import ctypes
+import math
 import os
 import subprocess
 
@@ -158,6 +170,40 @@ def linear(x: np.ndarray, pk: np.ndarray, sc: np.ndarray, group: int = GROUP) ->
     if np.asarray(x).dtype == np.float32:
         return matmul_f32x(x, w)
     return matmul_f32(x, w)
+
+
+SQRT_2_OVER_PI = math.sqrt(2.0 / math.pi)
+
+
+def gelu_tanh(g) -> np.ndarray:
+    """0.5 g (1 + tanh(z)), z = sqrt(2/pi) (g + 0.044715 g^3), in float64, evaluated as
+    g / (1 + exp(-2 z)) (the same function: 0.5 (1 + tanh z) = 1 / (1 + e^(-2z))).  The
+    literal tanh form cancels once 1 + tanh(z) < ~1e-16 (g below about -5.5) and loses
+    every digit of the negative tail; this form keeps full relative precision there."""
+    g = np.asarray(g, dtype=np.float64)
+    z = SQRT_2_OVER_PI * (g + 0.044715 * g ** 3)
+    with np.errstate(over="ignore"):
+        return g / (1.0 + np.exp(-2.0 * z))
+
+
+def gate_up_gelu(x: np.ndarray, pk_g: np.ndarray, sc_g: np.ndarray, pk_u: np.ndarray, sc_u: np.ndarray,
+                 group: int = GROUP, bf16_dots: bool = False):
+    """h[M, F] = gelu(x . Wg^T) * (x . Wu^T) with float64 dots (the exact values the fp32
+    kernels approximate) and the error-bound magnitudes sum |x||w| of each dot.
+    bf16_dots: g and u rounded to bf16 first (dotPrec with fam = bf16, engine.zig:531).
+    Returns (h64, g64, u64, mag_g, mag_u)."""
+    wg, wu = dequant(pk_g, sc_g, group), dequant(pk_u, sc_u, group)
+    if np.asarray(x).dtype == np.float32:
+        g, mg = matmul_f32x(x, wg, f64=True)
+        u, mu = matmul_f32x(x, wu, f64=True)
+    else:
+        g, mg = matmul_f64(x, wg)
+        u, mu = matmul_f64(x, wu)
+    if bf16_dots:
+        gr = bf16_to_f32(round_bf16(g.astype(np.float32))).astype(np.float64)
+        ur = bf16_to_f32(round_bf16(u.astype(np.float32))).astype(np.float64)
+        return gelu_tanh(gr) * ur, g, u, mg, mu
+    return gelu_tanh(g) * u, g, u, mg, mu
 
 
 def is_nan_bf16(h: np.ndarray) -> np.ndarray:

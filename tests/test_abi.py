@@ -127,3 +127,52 @@ def test_last_error_is_thread_local(L):
     t.join()
     assert seen["msg"] == ""
     assert "negative dimension" in L.w4a16_last_error().decode()
+
+
+def _gu(L, x=A, xd=0, pg=A, sg=A, pu=A, su=A, h=A, hd=0, M=1, F=16, K=256, group=32, flags=0, ws=None, wsb=0):
+    return L.w4a16_gate_up_gelu(x, xd, pg, sg, pu, su, h, hd, M, F, K, group, flags, ws, wsb, None)
+
+
+def test_gate_up_gelu_validation(L):
+    assert _gu(L, M=-1) == w4a16.EINVAL_SHAPE
+    assert _gu(L, K=60) == w4a16.EINVAL_SHAPE
+    assert _gu(L, K=96, group=64) == w4a16.EINVAL_SHAPE
+    assert _gu(L, F=2**30) == w4a16.EINVAL_SHAPE            # 16 * ceil(F / 8) virtual rows overflow int
+    assert _gu(L, group=48) == w4a16.EINVAL_ARG
+    assert _gu(L, xd=3) == w4a16.EINVAL_ARG
+    assert _gu(L, hd=5) == w4a16.EINVAL_ARG
+    assert _gu(L, flags=2) == w4a16.EINVAL_ARG
+    for kw in ("x", "pg", "sg", "pu", "su", "h"):
+        assert _gu(L, **{kw: None}) == w4a16.EINVAL_PTR, kw
+        assert _gu(L, **{kw: MIS}) == w4a16.EINVAL_PTR, kw
+    # the unfused route (K % 256 != 0 at M <= 64) needs f32 g and u in the workspace
+    assert _gu(L, M=8, K=320) == w4a16.EWORKSPACE
+    assert "workspace" in L.w4a16_last_error().decode()
+    assert _gu(L, xd=1) == w4a16.EWORKSPACE                  # f32 x: the split
+    assert _gu(L, ws=MIS, wsb=1024) == w4a16.EINVAL_PTR
+    assert _gu(L, M=0, x=None, pg=None, sg=None, pu=None, su=None, h=None) == 0
+    assert _gu(L, F=0, x=None, pg=None, sg=None, pu=None, su=None, h=None) == 0
+    assert L.w4a16_last_error().decode() == ""
+
+
+@pytest.mark.parametrize("M,F,K,xd,fused", [
+    (1, 15360, 3840, 0, True),     # 12B decode: straight-line GEMV
+    (4, 15360, 3840, 0, True),     # M = 4 at K = 3840: x too large for the GEMV plan -> skinny
+    (2, 6144, 1536, 0, True),      # E2B
+    (64, 15360, 3840, 0, True),    # skinny
+    (2048, 15360, 3840, 0, True),  # prefill
+    (300, 130, 192, 0, True),      # prefill, K % 256 != 0
+    (8, 40, 320, 0, False),        # K % 256 != 0 at M <= 64
+    (2, 24, 96, 0, False),
+    (1, 72, 1024, 1, True),        # f32 x in the decode GEMV
+    (8, 40, 512, 1, False),        # f32 x above M = 4
+])
+def test_gate_up_workspace_size(L, M, F, K, xd, fused):
+    n = L.w4a16_gate_up_workspace_size(M, F, K, xd)
+    split = L.w4a16_workspace_size(M, F, K, xd)
+    assert n % 256 == 0
+    if fused:
+        assert n == split
+    else:
+        assert n >= split + 8 * M * F
+    assert L.w4a16_gate_up_workspace_size(0, F, K, xd) == 0

@@ -10,6 +10,7 @@ closed forms.  Planted-mistake checks show each gate can fail.
 from __future__ import annotations
 
 import hashlib
+import math
 
 import numpy as np
 import pytest
@@ -252,3 +253,102 @@ def test_bf16_round_matches_torch():
     got = o.round_bf16(v)
     ref = _bf16_np(torch.from_numpy(v).to(torch.bfloat16))
     assert np.array_equal(got, ref)
+
+
+# ------------------------------------------------------------------ MLP front half
+# engine.zig:653: dot(xff, gate).gelu().mul(dot(xff, up)); Tensor.gelu = gelu_pytorch_tanh
+# (docs/ROADMAP_to_full_forward.md:30).  ZML is not vendored in the reference, so the
+# activation is pinned against torch's independent implementation of the same function
+# (the HF ACT2FN["gelu_pytorch_tanh"] the reference's MLP gate used as its oracle,
+# PLANNING.md:345) and against closed forms.
+
+def test_gelu_tanh_matches_torch_gelu_tanh():
+    """Against torch's float64 gelu(approximate="tanh"), which evaluates the literal tanh
+    form: equal to its rounding (absolute eps64 |g| from the cancelling 1 + tanh)."""
+    rng = np.random.default_rng(5)
+    g = np.concatenate([rng.standard_normal(20_000) * 3, rng.uniform(-40, 40, 20_000),
+                        [0.0, -0.0, 1e-30, -1e-30, 1e4, -1e4]])
+    ref = torch.nn.functional.gelu(torch.from_numpy(g), approximate="tanh").numpy()
+    got = o.gelu_tanh(g)
+    assert np.all(np.abs(got - ref) <= 4e-16 * np.maximum(1e-300, np.abs(g)) + 1e-300)
+
+
+def _gelu_tanh_decimal(g: float) -> float:
+    """The defining formula 0.5 g (1 + tanh z) with tanh z = (e^2z - 1) / (e^2z + 1), in
+    400-digit decimal arithmetic (no float cancellation down to g = -20)."""
+    from decimal import Decimal, getcontext
+    getcontext().prec = 400
+    G = Decimal(g)
+    c = (Decimal(2) / Decimal("3.14159265358979323846264338327950288419716939937510582097494")).sqrt()
+    z = c * (G + Decimal("0.044715") * G ** 3)
+    e2 = (2 * z).exp()
+    return float(Decimal("0.5") * G * (1 + (e2 - 1) / (e2 + 1)))
+
+
+def test_gelu_tanh_negative_tail_vs_high_precision():
+    """Where the float tanh form has no correct digit left (g < -5.5) the oracle still
+    matches the definition to float64 precision (far below fp32's)."""
+    for g in [-1.0, -3.0, -5.5, -6.7, -8.37, -9.7, -12.0, -20.0, 0.3, 2.0, 7.0]:
+        ref = _gelu_tanh_decimal(g)
+        got = float(o.gelu_tanh(g))
+        # exp amplifies the argument's rounding: relative error <= (8 + 16 |z|) eps64
+        z = math.sqrt(2 / math.pi) * abs(g + 0.044715 * g ** 3)
+        assert abs(got - ref) <= (8 + 16 * z) * 2.0 ** -52 * abs(ref) + 1e-320, (g, got, ref)
+    # the float tanh form fails this at g = -8.37 (it returns 0): the check can see it
+    t = 0.5 * -8.37 * (1 + math.tanh(math.sqrt(2 / math.pi) * (-8.37 + 0.044715 * -8.37 ** 3)))
+    assert abs(t - _gelu_tanh_decimal(-8.37)) > 0.5 * abs(_gelu_tanh_decimal(-8.37))
+
+
+def test_gelu_tanh_closed_forms():
+    # odd part: gelu(x) - gelu(-x) = 0.5x(1+t) + 0.5x(1-t) = x for every x
+    x = np.linspace(-12, 12, 2401)
+    assert np.max(np.abs(o.gelu_tanh(x) - o.gelu_tanh(-x) - x)) <= 1e-14 * 12
+    assert o.gelu_tanh(0.0) == 0.0
+    # value at 1 from the definition with the constants written out independently
+    z = math.sqrt(2 / math.pi) * (1 + 0.044715)
+    assert abs(float(o.gelu_tanh(1.0)) - 0.5 * (1 + math.tanh(z))) <= 1e-16
+    # the tanh form, not the erf form (0.841344746...): they differ by ~1.5e-4 at 1
+    erf_form = 0.5 * (1 + math.erf(1 / math.sqrt(2)))
+    assert abs(float(o.gelu_tanh(1.0)) - erf_form) > 1e-4
+    # limits: identity for large g, 0 for very negative g
+    assert abs(float(o.gelu_tanh(30.0)) - 30.0) <= 1e-12
+    assert abs(float(o.gelu_tanh(-30.0))) <= 1e-30
+
+
+def _torch_mlp_front(x_u16, pk_g, sc_g, pk_u, sc_u):
+    """gelu(gate) * up with torch only: bf16 multiply dequant, float64 matmul, torch gelu."""
+    def wt(pk, sc):
+        q = torch.from_numpy(o.unpack(pk).astype(np.float32)).to(torch.bfloat16)
+        s = torch.from_numpy(sc.view(np.int16)).view(torch.bfloat16)
+        return (q * s.repeat_interleave(32, dim=1)).double()
+    x = torch.from_numpy(x_u16.view(np.int16)).view(torch.bfloat16).double()
+    g = x @ wt(pk_g, sc_g).T
+    u = x @ wt(pk_u, sc_u).T
+    return torch.nn.functional.gelu(g, approximate="tanh") * u, g, u
+
+
+def test_gate_up_gelu_matches_torch_composition():
+    _, pk_g, sc_g = o.synth_weights(40, 256, 71)
+    _, pk_u, sc_u = o.synth_weights(40, 256, 72)
+    x = o.synth_x(3, 256, 73)
+    h, g, u, mg, mu = o.gate_up_gelu(x, pk_g, sc_g, pk_u, sc_u)
+    ref, rg, ru = _torch_mlp_front(x, pk_g, sc_g, pk_u, sc_u)
+    assert np.allclose(g, rg.numpy(), rtol=0, atol=1e-12) and np.allclose(u, ru.numpy(), rtol=0, atol=1e-12)
+    assert np.all(mg >= np.abs(g)) and np.all(mu >= np.abs(u))
+    assert np.max(np.abs(h - ref.numpy())) <= 1e-12 * max(1.0, float(np.max(np.abs(h))))
+    # planted mistakes the check must see: gelu(gate * up), gelu(up) * gate
+    assert np.max(np.abs(o.gelu_tanh(g * u) - ref.numpy())) > 1e-3
+    assert np.max(np.abs(o.gelu_tanh(u) * g - ref.numpy())) > 1e-3
+
+
+def test_gate_up_gelu_bf16_dots_rounds_both_dots():
+    _, pk_g, sc_g = o.synth_weights(24, 128, 81)
+    _, pk_u, sc_u = o.synth_weights(24, 128, 82)
+    x = o.synth_x(2, 128, 83)
+    h, g, u, _, _ = o.gate_up_gelu(x, pk_g, sc_g, pk_u, sc_u, bf16_dots=True)
+    gb = torch.from_numpy(g).float().to(torch.bfloat16).double()
+    ub = torch.from_numpy(u).float().to(torch.bfloat16).double()
+    ref = torch.nn.functional.gelu(gb, approximate="tanh") * ub
+    assert np.max(np.abs(h - ref.numpy())) <= 1e-12 * max(1.0, float(np.max(np.abs(h))))
+    h_plain = o.gate_up_gelu(x, pk_g, sc_g, pk_u, sc_u)[0]
+    assert np.max(np.abs(h - h_plain)) > 0
