@@ -95,10 +95,19 @@ def graph_of(torch, fn):
     return g
 
 
-def time_graph(torch, g, replays, warmup=2):
-    for _ in range(warmup):
+def steady(torch, g, seconds=0.3, min_replays=2):
+    """Replay g untimed until `seconds` of wall time have passed: the first
+    milliseconds of a heavy run are slower (clock ramp-up) by up to ~15 %."""
+    t0 = time.perf_counter()
+    n = 0
+    while n < min_replays or time.perf_counter() - t0 < seconds:
         g.replay()
-    torch.cuda.synchronize()
+        torch.cuda.synchronize()
+        n += 1
+
+
+def time_graph(torch, g, replays, warmup=2):
+    steady(torch, g, min_replays=warmup)
     a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     a.record()
     for _ in range(replays):
@@ -210,10 +219,12 @@ def time_gate_up(torch, w4a16, o, M, K, F):
             torch.mul(torch.nn.functional.gelu(y[:, :F], approximate="tanh"), y[:, F:], out=h)
 
     out = {"M": M, "K": K, "F": F, "bytes": nbytes, "flops": 4 * M * F * K, "sets": nsets, "launches": launches}
-    for name, fn in (("fused", fused), ("unfused", unfused)):
-        g = graph_of(torch, fn)
-        out[name + "_us"] = time_graph(torch, g, reps) / (reps * launches) * 1e6
-        del g
+    graphs = {name: graph_of(torch, fn) for name, fn in (("fused", fused), ("unfused", unfused))}
+    for _ in range(2):  # alternate the legs and keep each one's best, so that order effects cancel
+        for name, g in graphs.items():
+            t = time_graph(torch, g, reps) / (reps * launches) * 1e6
+            out[name + "_us"] = min(out.get(name + "_us", t), t)
+    del graphs
     del sets, lins
     torch.cuda.empty_cache()
     t = out["fused_us"] * 1e-6
@@ -323,9 +334,7 @@ def main() -> int:
     # replayed until `steps` steps have run, bracketed by synchronize + events
     g = graph_of(torch, lambda: [step(s) for s in range(nsets)])
     reps = max(1, -(-args.steps // nsets))
-    for _ in range(2):
-        g.replay()
-    torch.cuda.synchronize()
+    steady(torch, g)
     e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     t0 = time.perf_counter()
     e0.record()

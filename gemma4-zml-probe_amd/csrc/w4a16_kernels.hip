@@ -831,8 +831,13 @@ constexpr int SK_P = 4;  // weight prefetch depth (chunks); even, for the two-sl
 template <int MT, bool G32>
 __global__ void __launch_bounds__(256) skinny_kernel(SkinnyArgs a) {
   constexpr int P = SK_P;
-  constexpr int XPAD = 8;  // halves of padding per LDS row
-  __shared__ __attribute__((aligned(16))) uint16_t xs[2][16 * MT][256 + XPAD];
+  // x rows of 256 halves as 4 groups of 64 (one lane group c each), every group padded
+  // to 72 halves and every row to 304: the A-fragment reads (16 rows, lane groups
+  // 144 B apart) are then free of LDS bank conflicts (measured on gfx950: a 16-byte
+  // row pad with groups 128 B apart reads 18 % slower), and every (v, j) read is an
+  // immediate offset from one address per lane.
+  constexpr int XG = 72, XROW = 304;
+  __shared__ __attribute__((aligned(16))) uint16_t xs[2][16 * MT][XROW];
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int r = lane & 15, c = lane >> 4;
@@ -878,7 +883,8 @@ __global__ void __launch_bounds__(256) skinny_kernel(SkinnyArgs a) {
     for (int i = 0; i < XV; ++i) {
       const int v = (int)threadIdx.x + 256 * i;
       const int row = v >> 5, col = (v & 31) * 8;
-      *reinterpret_cast<u32x4*>(&xs[buf][row][col]) = u32x4{xr[4 * i], xr[4 * i + 1], xr[4 * i + 2], xr[4 * i + 3]};
+      *reinterpret_cast<u32x4*>(&xs[buf][row][(col >> 6) * XG + (col & 63)]) =
+          u32x4{xr[4 * i], xr[4 * i + 1], xr[4 * i + 2], xr[4 * i + 3]};
     }
   };
 
@@ -912,7 +918,7 @@ __global__ void __launch_bounds__(256) skinny_kernel(SkinnyArgs a) {
       for (int j = 0; j < 4; ++j)
 #pragma unroll
         for (int mt = 0; mt < MT; ++mt)
-          xa[j][mt] = *reinterpret_cast<const bf16x8*>(&xs[buf][16 * mt + r][(c * 2 + v) * 32 + 8 * j]);
+          xa[j][mt] = *reinterpret_cast<const bf16x8*>(&xs[buf][16 * mt + r][c * XG + v * 32 + 8 * j]);
       __builtin_amdgcn_sched_barrier(0);
       const uint32_t wj[4] = {wv[slot][v].x, wv[slot][v].y, wv[slot][v].z, wv[slot][v].w};
 #pragma unroll
@@ -1020,9 +1026,8 @@ struct PrefillArgs {
   int bf16_dots;
 };
 
-template <int TN, int P, bool G32>
+template <int TN, int P, bool G32, int MB = 8>  // MB: 32-row blocks of x per workgroup
 __global__ void __launch_bounds__(256) prefill_kernel(PrefillArgs a) {
-  constexpr int MB = 8;            // 32-row blocks of x per workgroup
   constexpr int BM = 32 * MB;
   constexpr int BN = 4 * 32 * TN;
   constexpr int XPAD = 8;
@@ -1521,7 +1526,12 @@ hipError_t w4l_skinny(const uint16_t* x, const int32_t* pk, const uint16_t* sc, 
   a.groups_per_row = (int)(K / group);
   a.y_f32 = y_f32;
   a.nk = (int)(K / 256);
-  const int mt = M <= 16 ? 1 : M <= 32 ? 2 : 4;
+  int mt = M <= 16 ? 1 : M <= 32 ? 2 : 4;
+  // W4A16_SKINNY_MT=<1|2|4>: tuning override of the 16-row x tiles per workgroup
+  if (const char* e = getenv("W4A16_SKINNY_MT")) {
+    const int v = atoi(e);
+    if (v == 1 || v == 2 || v == 4) mt = v;
+  }
   const dim3 grid((unsigned)((N + 63) / 64), (unsigned)((M + 16 * mt - 1) / (16 * mt))), block(256);
   const bool g32 = group == 32;
 #define W4_SK(MT_)                                                                                   \
@@ -1561,19 +1571,25 @@ hipError_t w4l_prefill(const uint16_t* x, const int32_t* pk, const uint16_t* sc,
   a.groups_per_row = (int)(K / group);
   a.y_f32 = y_f32;
   a.ns = (int)(K / 64);
-  a.mblk = (int)((M + 255) / 256);
+  // x rows per workgroup: 64 / 128 / 256 (MB = 2 / 4 / 8 blocks of 32), the smallest that
+  // holds M, so small M pays no MFMAs on padding rows
+  const int mb = M <= 64 ? 2 : M <= 128 ? 4 : 8;
+  a.mblk = (int)((M + 32 * mb - 1) / (32 * mb));
   // two W blocks of 32 rows per wave when that still leaves two workgroups per CU
-  const bool tn2 = ((N + 255) / 256) * a.mblk >= 512;
+  const bool tn2 = mb == 8 && ((N + 255) / 256) * a.mblk >= 512;
   const int bn = tn2 ? 256 : 128;
   const dim3 grid((unsigned)(((N + bn - 1) / bn) * a.mblk)), block(256);
   const bool g32 = group == 32;
-  if (tn2) {
-    if (g32) hipLaunchKernelGGL((w4k::prefill_kernel<2, 2, true>), grid, block, 0, st, a);
-    else hipLaunchKernelGGL((w4k::prefill_kernel<2, 2, false>), grid, block, 0, st, a);
-  } else {
-    if (g32) hipLaunchKernelGGL((w4k::prefill_kernel<1, 4, true>), grid, block, 0, st, a);
-    else hipLaunchKernelGGL((w4k::prefill_kernel<1, 4, false>), grid, block, 0, st, a);
-  }
+#define W4_PF(TN_, P_, MB_)                                                                         \
+  do {                                                                                              \
+    if (g32) hipLaunchKernelGGL((w4k::prefill_kernel<TN_, P_, true, MB_>), grid, block, 0, st, a);  \
+    else hipLaunchKernelGGL((w4k::prefill_kernel<TN_, P_, false, MB_>), grid, block, 0, st, a);     \
+  } while (0)
+  if (tn2) W4_PF(2, 2, 8);
+  else if (mb == 8) W4_PF(1, 4, 8);
+  else if (mb == 4) W4_PF(1, 4, 4);
+  else W4_PF(1, 4, 2);
+#undef W4_PF
   return hipGetLastError();
 }
 
@@ -1582,6 +1598,9 @@ hipError_t w4l_linear(const uint16_t* x_planes, int nterms, const int32_t* pk, c
                       hipStream_t st) {
   if (w4l_gemv_ok(M, K, nterms)) return w4l_gemv(x_planes, nterms, pk, sc, y, y_f32, M, N, K, group, st);
   if (w4l_prefill_ok(M, K, nterms)) return w4l_prefill(x_planes, pk, sc, y, y_f32, M, N, K, group, st);
+  // W4A16_PF_SMALL=1: tuning switch, 16 < M <= 64 through the 32x32 kernel with 64 rows of x
+  if (getenv("W4A16_PF_SMALL") && nterms == 1 && M > 16 && K % 64 == 0)
+    return w4l_prefill(x_planes, pk, sc, y, y_f32, M, N, K, group, st);
   if (w4l_skinny_ok(M, K, nterms)) return w4l_skinny(x_planes, pk, sc, y, y_f32, M, N, K, group, st);
   const W4Plan p = w4l_plan(M, N, K, nterms);
   w4k::LinearArgs a{};

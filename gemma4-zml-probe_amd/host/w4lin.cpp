@@ -117,6 +117,34 @@ void W4Lin::linear_f32(const float* x, float* y, int64_t m, void* workspace, siz
         "W4Lin.linear_f32");
 }
 
+namespace {
+void gate_up_call(const W4Lin& gate, const W4Lin& up, const uint16_t* x, void* h, int32_t h_dtype, int64_t m,
+                  void* workspace, size_t ws_bytes, hipStream_t stream, bool bf16_dots) {
+  if (up.n != gate.n || up.k != gate.k || up.group != gate.group)
+    throw Error(W4A16_EINVAL_SHAPE, "gate_up_gelu: up [" + std::to_string(up.n) + ", " + std::to_string(up.k) +
+                                        "] / group " + std::to_string(up.group) + " does not match gate [" +
+                                        std::to_string(gate.n) + ", " + std::to_string(gate.k) + "] / group " +
+                                        std::to_string(gate.group));
+  check(w4a16_gate_up_gelu(x, W4A16_DTYPE_BF16, gate.pk, gate.sc, up.pk, up.sc, h, h_dtype, m, gate.n, gate.k,
+                           gate.group, bf16_dots ? W4A16_GATE_UP_BF16_DOTS : 0, workspace, ws_bytes, stream),
+        "gate_up_gelu");
+}
+}  // namespace
+
+size_t gate_up_workspace(const W4Lin& gate, int64_t m) {
+  return w4a16_gate_up_workspace_size(m, gate.n, gate.k, W4A16_DTYPE_BF16);
+}
+
+void gate_up_gelu(const W4Lin& gate, const W4Lin& up, const uint16_t* x, uint16_t* h, int64_t m, void* workspace,
+                  size_t ws_bytes, hipStream_t stream, bool bf16_dots) {
+  gate_up_call(gate, up, x, h, W4A16_DTYPE_BF16, m, workspace, ws_bytes, stream, bf16_dots);
+}
+
+void gate_up_gelu(const W4Lin& gate, const W4Lin& up, const uint16_t* x, float* h, int64_t m, void* workspace,
+                  size_t ws_bytes, hipStream_t stream, bool bf16_dots) {
+  gate_up_call(gate, up, x, h, W4A16_DTYPE_F32, m, workspace, ws_bytes, stream, bf16_dots);
+}
+
 Census census(const SafeTensorsFile& f) {
   Census c;
   for (const auto& kv : f.tensors()) {

@@ -81,6 +81,17 @@ struct W4Lin {
   void linear_f32(const float* x, float* y, int64_t m, void* workspace, size_t ws_bytes, hipStream_t stream) const;
 };
 
+// The MLP front half (engine.zig:653, dotPrec(xff, gate).gelu().mul(dotPrec(xff, up))):
+// h[m, F] = gelu_tanh(x . gate.toW()^T) * (x . up.toW()^T) in one call; gate and up
+// must both be [F, K] with the same group.  bf16_dots rounds both dot outputs to
+// bf16 first (dotPrec with fam = bf16).  Shapes that no fused kernel takes need
+// gate_up_workspace(gate, m) bytes of caller workspace (0 on the Gemma shapes).
+size_t gate_up_workspace(const W4Lin& gate, int64_t m);
+void gate_up_gelu(const W4Lin& gate, const W4Lin& up, const uint16_t* x, uint16_t* h, int64_t m, void* workspace,
+                  size_t ws_bytes, hipStream_t stream, bool bf16_dots = false);
+void gate_up_gelu(const W4Lin& gate, const W4Lin& up, const uint16_t* x, float* h, int64_t m, void* workspace,
+                  size_t ws_bytes, hipStream_t stream, bool bf16_dots = false);
+
 // ---------------------------------------------------------------- checkpoint census
 struct CensusEntry {
   std::string name;  // module name, without ".weight_packed"

@@ -10,6 +10,8 @@
 //       receives M*n bf16 (default) or f32 values.
 //   w4lin_tool dequant <file.safetensors> <name> <w.bin>
 //       w[n, k] = toW() (bf16) on the GPU.
+//   w4lin_tool mlp <file.safetensors> <gate> <up> <M> <x.bin> <h.bin> [bf16|f32]
+//       h[M, F] = gelu_tanh(x . gate^T) * (x . up^T) on the GPU (engine.zig:653).
 #include <hip/hip_runtime.h>
 
 #include <cstdio>
@@ -29,7 +31,8 @@ int usage() {
                "usage: w4lin_tool census <file> [--expect N]\n"
                "       w4lin_tool layer12 <file> <prefix> <j>\n"
                "       w4lin_tool linear <file> <name> <M> <x.bin> <y.bin> [bf16|f32]\n"
-               "       w4lin_tool dequant <file> <name> <w.bin>\n");
+               "       w4lin_tool dequant <file> <name> <w.bin>\n"
+               "       w4lin_tool mlp <file> <gate> <up> <M> <x.bin> <h.bin> [bf16|f32]\n");
   return 2;
 }
 
@@ -129,6 +132,35 @@ int cmd_linear(int argc, char** argv) {
   return 0;
 }
 
+int cmd_mlp(int argc, char** argv) {
+  if (argc < 8) return usage();
+  const bool f32 = argc > 8 && !std::strcmp(argv[8], "f32");
+  const int64_t M = std::atoll(argv[5]);
+  w4::DeviceStore store(argv[2]);
+  const w4::W4Lin gate = w4::W4Lin::init(store, argv[3]);
+  const w4::W4Lin up = w4::W4Lin::init(store, argv[4]);
+  const auto x = read_file(argv[6], (size_t)(M * gate.k * 2));
+  const size_t hbytes = (size_t)(M * gate.n * (f32 ? 4 : 2));
+  const size_t ws = w4::gate_up_workspace(gate, M);
+  void *dx = nullptr, *dh = nullptr, *dws = nullptr;
+  hip_ok(hipMalloc(&dx, std::max<size_t>(x.size(), 16)), "hipMalloc x");
+  hip_ok(hipMalloc(&dh, std::max<size_t>(hbytes, 16)), "hipMalloc h");
+  if (ws) hip_ok(hipMalloc(&dws, ws), "hipMalloc workspace");
+  hip_ok(hipMemcpy(dx, x.data(), x.size(), hipMemcpyHostToDevice), "copy x");
+  if (f32) w4::gate_up_gelu(gate, up, static_cast<const uint16_t*>(dx), static_cast<float*>(dh), M, dws, ws, nullptr);
+  else w4::gate_up_gelu(gate, up, static_cast<const uint16_t*>(dx), static_cast<uint16_t*>(dh), M, dws, ws, nullptr);
+  std::vector<char> h(hbytes);
+  hip_ok(hipMemcpy(h.data(), dh, hbytes, hipMemcpyDeviceToHost), "copy h");
+  write_file(argv[7], h.data(), hbytes);
+  (void)hipFree(dx);
+  (void)hipFree(dh);
+  if (dws) (void)hipFree(dws);
+  std::printf("{\"gate\": \"%s\", \"up\": \"%s\", \"M\": %lld, \"F\": %lld, \"k\": %lld, \"workspace\": %zu, \"h\": \"%s\"}\n",
+              json_escape(argv[3]).c_str(), json_escape(argv[4]).c_str(), (long long)M, (long long)gate.n,
+              (long long)gate.k, ws, f32 ? "f32" : "bf16");
+  return 0;
+}
+
 int cmd_dequant(int argc, char** argv) {
   if (argc < 5) return usage();
   w4::DeviceStore store(argv[2]);
@@ -154,6 +186,7 @@ int main(int argc, char** argv) {
     if (cmd == "layer12") return cmd_layer12(argc, argv);
     if (cmd == "linear") return cmd_linear(argc, argv);
     if (cmd == "dequant") return cmd_dequant(argc, argv);
+    if (cmd == "mlp") return cmd_mlp(argc, argv);
     return usage();
   } catch (const w4::Error& e) {
     std::fprintf(stderr, "w4lin_tool: %s (status %d)\n", e.what(), e.status());

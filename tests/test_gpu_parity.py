@@ -469,3 +469,20 @@ def test_gemv_tiles_per_workgroup(N, tpw, monkeypatch):
     yb = gpu_linear(x, pk, sc, "bf16")
     _, mag = o.matmul_f64(x, w)
     check_bf16(yb, ref32, mag, K)
+
+
+@pytest.mark.parametrize("M,N,K", [(17, 200, 1536), (32, 130, 640), (48, 2048, 1536), (64, 300, 3840)])
+def test_prefill_kernel_small_m(M, N, K, monkeypatch):
+    """The 32x32 kernel with 64 rows of x per workgroup (W4A16_PF_SMALL routes
+    16 < M <= 64 to it), including x rows past M and ragged N."""
+    monkeypatch.setenv("W4A16_PF_SMALL", "1")
+    _, pk, sc = o.synth_weights(N, K, 45)
+    x = o.synth_x(M, K, 46)
+    w = o.dequant(pk, sc)
+    ref32 = o.matmul_f32(x, w)
+    say(f"prefill kernel, small M: M={M} N={N} K={K}")
+    y = gpu_linear(x, pk, sc, "f32")
+    check_f32(y, x, w, K, ref32)
+    yb = gpu_linear(x, pk, sc, "bf16")
+    _, mag = o.matmul_f64(x, w)
+    check_bf16(yb, ref32, mag, K)

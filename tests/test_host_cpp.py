@@ -191,3 +191,53 @@ def test_cpp_w4lin_linear_and_dequant_on_gpu(tool, tmp_path, M, out):
         y = o.bf16_to_f32(np.fromfile(tmp_path / "y.bin", dtype=np.uint16).reshape(M, n)).astype(np.float64)
         ulp = 2.0 ** (np.floor(np.log2(np.maximum(np.abs(ref32), 2.0 ** -126))) - 7)
         assert np.all(np.abs(y - ref32) <= ulp + 2 * gam * mag)
+
+
+@pytest.mark.gpu
+def test_cpp_mlp_rejects_mismatched_up(tool, tmp_path):
+    """gate [32, 64] with up [16, 64]: gate_up_gelu throws before any kernel runs (W4Lin.init
+    uploads the weights first, hence the GPU mark)."""
+    if not torch.cuda.is_available():
+        pytest.skip("no GPU")
+    t = {f"g.{k}": v for k, v in packed_linear(32, 64, 1).items()}
+    t.update({f"u.{k}": v for k, v in packed_linear(16, 64, 2).items()})
+    path = str(tmp_path / "mm.safetensors")
+    save_file(t, path)
+    (tmp_path / "x.bin").write_bytes(b"\0" * (2 * 64))
+    rc, _, err = run(tool, "mlp", path, "g", "u", 1, tmp_path / "x.bin", tmp_path / "h.bin")
+    assert rc == 3 and "does not match gate" in err
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("M,out", [(1, "f32"), (3, "bf16"), (70, "f32"), (8, "bf16")])
+def test_cpp_gate_up_gelu_on_gpu(tool, tmp_path, M, out):
+    """gate_up_gelu through the C++ mirror (both fused routes and, at K = 320, M = 8, the
+    unfused one with tool-allocated workspace) against the oracle, with the bound of
+    tests/test_gpu_gate_up.py."""
+    if not torch.cuda.is_available():
+        pytest.skip("no GPU")
+    from test_gpu_gate_up import bound, ulp_bf16
+    F, K = 72, (320 if M == 8 else 512)
+    t = {f"mlp.gate_proj.{kk}": v for kk, v in packed_linear(F, K, 11).items()}
+    t.update({f"mlp.up_proj.{kk}": v for kk, v in packed_linear(F, K, 12).items()})
+    path = str(tmp_path / "mlp.safetensors")
+    save_file(t, path)
+    x = o.synth_x(M, K, 13)
+    x.tofile(tmp_path / "x.bin")
+    rc, outp, err = run(tool, "mlp", path, "mlp.gate_proj", "mlp.up_proj", M, tmp_path / "x.bin",
+                        tmp_path / "h.bin", out)
+    assert rc == 0, err
+    ws = json.loads(outp)["workspace"]
+    assert (ws > 0) if M == 8 else (ws == 0)  # K = 320 at M = 8 takes the unfused route
+    pg = t["mlp.gate_proj.weight_packed"].numpy()
+    sg = t["mlp.gate_proj.weight_scale"].view(torch.int16).numpy().view(np.uint16)
+    pu = t["mlp.up_proj.weight_packed"].numpy()
+    su = t["mlp.up_proj.weight_scale"].view(torch.int16).numpy().view(np.uint16)
+    h64, g, u, mg, mu = o.gate_up_gelu(x, pg, sg, pu, su)
+    b = bound(g, u, mg, mu, K, False)
+    if out == "f32":
+        h = np.fromfile(tmp_path / "h.bin", dtype=np.float32).reshape(M, F).astype(np.float64)
+    else:
+        h = o.bf16_to_f32(np.fromfile(tmp_path / "h.bin", dtype=np.uint16).reshape(M, F)).astype(np.float64)
+        b = b + ulp_bf16(np.abs(h64) + b)
+    assert np.all(np.abs(h - h64) <= b)
