@@ -191,7 +191,7 @@ def cpu_baseline(budget_s: float = 15.0):
                       f"{med * 1e3:.1f} ms/step; os.cpu_count()={os.cpu_count()}; cpu={cpu_model}"}
 
 
-def time_gate_up(torch, w4a16, o, M, K, F):
+def time_gate_up(torch, w4a16, o, M, K, F, unfused_leg=True):
     """Average duration of one fused w4a16_gate_up_gelu launch (h bf16 [M, F]) against the
     unfused composition (one linear over the concatenated [2F, K] weight, then torch's
     gelu(approximate="tanh") * mul on the bf16 halves), both as HIP graphs over weight sets
@@ -219,7 +219,8 @@ def time_gate_up(torch, w4a16, o, M, K, F):
             torch.mul(torch.nn.functional.gelu(y[:, :F], approximate="tanh"), y[:, F:], out=h)
 
     out = {"M": M, "K": K, "F": F, "bytes": nbytes, "flops": 4 * M * F * K, "sets": nsets, "launches": launches}
-    graphs = {name: graph_of(torch, fn) for name, fn in (("fused", fused), ("unfused", unfused))}
+    legs = (("fused", fused), ("unfused", unfused)) if unfused_leg else (("fused", fused),)
+    graphs = {name: graph_of(torch, fn) for name, fn in legs}
     for _ in range(2):  # alternate the legs and keep each one's best, so that order effects cancel
         for name, g in graphs.items():
             t = time_graph(torch, g, reps) / (reps * launches) * 1e6
@@ -249,6 +250,8 @@ def main() -> int:
     ap.add_argument("--gate-up", type=str, default=None,
                     help="M,K,F: time only the fused gate/up + gelu*mul call (w4a16_gate_up_gelu) against the "
                          "unfused composition; the workload of the gate/up rocprofv3 summaries")
+    ap.add_argument("--no-unfused", action="store_true",
+                    help="with --gate-up: time only the fused call (the workload of its kernel traces)")
     ap.add_argument("--copy-calibration", action="store_true",
                     help="run only a plain device copy of known size (256 MiB read + 256 MiB write, 20 times): "
                          "the scale for rocprofv3 FETCH_SIZE / WRITE_SIZE")
@@ -289,9 +292,10 @@ def main() -> int:
 
     if args.gate_up:
         gM, gK, gF = (int(v) for v in args.gate_up.split(","))
-        r = time_gate_up(torch, w4a16, o, gM, gK, gF)
+        r = time_gate_up(torch, w4a16, o, gM, gK, gF, unfused_leg=not args.no_unfused)
         print(json.dumps({"M": gM, "K": gK, "F": gF, "bytes_per_launch": r["bytes"], "flops_per_launch": r["flops"],
-                          "fused_us": round(r["fused_us"], 3), "unfused_us": round(r["unfused_us"], 3),
+                          "fused_us": round(r["fused_us"], 3),
+                          "unfused_us": round(r["unfused_us"], 3) if "unfused_us" in r else None,
                           "GBps": round(r["GBps"], 1), "TFLOPs": round(r["TFLOPs"], 2),
                           "launches_per_replay": r["launches"]}), flush=True)
         return 0
@@ -301,7 +305,7 @@ def main() -> int:
         r = time_config(torch, w4a16, o, 1, dK, dN)
         print(json.dumps({"kernel": DOMINANT_KERNEL, "M": 1, "K": dK, "N": dN, "bytes_per_launch": r["bytes"],
                           "avg_launch_us": round(r["us"], 3), "GBps": round(r["GBps"], 1),
-                          "launches_run": r["launches"] * 8}), flush=True)
+                          "launches_per_replay": r["launches"]}), flush=True)
         return 0
 
     # ---- the headline workload: 12B layer linears at M=1, rotating sets
@@ -379,6 +383,14 @@ def main() -> int:
             table.append(r)
             log(f"{name:12s} M={M:5d} K={K:6d} N={N:6d}  {r['us']:9.2f} us"
                 f"  {r['GBps']:8.1f} GB/s ({r['hbm_frac'] * 100:5.1f} %)  {r['TFLOPs']:8.2f} TFLOP/s ({r['mfma_frac'] * 100:5.1f} %)")
+        # fused gate/up + gelu*mul (engine.zig:653) against the unfused composition
+        for name, M, K, F in [("E2B_gelu", 1, 1536, 6144), ("12B_gelu", 1, 3840, 15360),
+                              ("12B_gelu", 64, 3840, 15360), ("12B_gelu", 2048, 3840, 15360)]:
+            r = time_gate_up(torch, w4a16, o, M, K, F)
+            r["name"] = name
+            table.append(r)
+            log(f"{name:12s} M={M:5d} K={K:6d} F={F:6d}  fused {r['fused_us']:9.2f} us  unfused {r['unfused_us']:9.2f} us"
+                f"  {r['GBps']:8.1f} GB/s  {r['TFLOPs']:8.2f} TFLOP/s")
         os.makedirs(os.path.join(ROOT, "gpurun_out"), exist_ok=True)
         with open(os.path.join(ROOT, "gpurun_out", "bench_all.json"), "w") as f:
             json.dump(table, f, indent=1)
