@@ -233,6 +233,33 @@ def time_gate_up(torch, w4a16, o, M, K, F, unfused_leg=True):
     return out
 
 
+def time_lm_head(torch, w4a16, o, M, V, K, k):
+    """Average duration of one w4a16_lm_head call (logits + softcap 30 + top-k) over one
+    bf16 [V, K] embedding (2 GB at the 12B shape, larger than the MALL), as a HIP graph of
+    back-to-back calls."""
+    g = torch.Generator(device="cuda")
+    g.manual_seed(9000)
+    e = (torch.randn((V, K), generator=g, device="cuda") * 0.05).to(torch.bfloat16)
+    x = synth_x_dev(torch, o, M, K)
+    logits = torch.empty((M, V), dtype=torch.float32, device="cuda")
+    ws = torch.empty(max(16, w4a16.lm_head_workspace_size(M, V, K, w4a16.DTYPE_BF16, k)), dtype=torch.uint8,
+                     device="cuda")
+    launches = 10
+
+    def run():
+        for _ in range(launches):
+            w4a16.lm_head(x, e, softcap=30.0, topk=k, logits=logits, workspace=ws)
+
+    gr = graph_of(torch, run)
+    reps = 3
+    t = time_graph(torch, gr, reps) / (reps * launches)
+    del gr, e
+    torch.cuda.empty_cache()
+    nbytes = V * K * 2 + M * K * 2 + M * V * 4
+    return {"M": M, "V": V, "K": K, "topk": k, "bytes": nbytes, "us": t * 1e6, "GBps": nbytes / t / 1e9,
+            "hbm_frac": nbytes / t / 1e9 / PEAK_HBM_GBS}
+
+
 def main() -> int:
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -250,6 +277,9 @@ def main() -> int:
     ap.add_argument("--gate-up", type=str, default=None,
                     help="M,K,F: time only the fused gate/up + gelu*mul call (w4a16_gate_up_gelu) against the "
                          "unfused composition; the workload of the gate/up rocprofv3 summaries")
+    ap.add_argument("--lm-head", type=str, default=None,
+                    help="M,V,K,k: time only the lm_head call (logits, softcap 30, top-k); the workload of "
+                         "its kernel traces")
     ap.add_argument("--no-unfused", action="store_true",
                     help="with --gate-up: time only the fused call (the workload of its kernel traces)")
     ap.add_argument("--copy-calibration", action="store_true",
@@ -298,6 +328,14 @@ def main() -> int:
                           "unfused_us": round(r["unfused_us"], 3) if "unfused_us" in r else None,
                           "GBps": round(r["GBps"], 1), "TFLOPs": round(r["TFLOPs"], 2),
                           "launches_per_replay": r["launches"]}), flush=True)
+        return 0
+
+    if args.lm_head:
+        hM, hV, hK, hk = (int(v) for v in args.lm_head.split(","))
+        r = time_lm_head(torch, w4a16, o, hM, hV, hK, hk)
+        print(json.dumps({"M": hM, "V": hV, "K": hK, "topk": hk, "bytes_per_call": r["bytes"],
+                          "avg_call_us": round(r["us"], 3), "GBps": round(r["GBps"], 1),
+                          "hbm_frac": round(r["hbm_frac"], 4)}), flush=True)
         return 0
 
     if args.only_dominant:

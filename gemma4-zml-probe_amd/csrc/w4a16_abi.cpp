@@ -218,4 +218,70 @@ int w4a16_gate_up_gelu(const void* x, int32_t x_dtype, const int32_t* pk_gate, c
   return hip_status(w4l_gelu_mul(g, u, h, h_f32, pair.bf16_dots, M * F, st), fn);
 }
 
+size_t w4a16_lm_head_workspace_size(int64_t M, int64_t V, int64_t K, int32_t x_dtype, int32_t topk) {
+  if (M <= 0 || V <= 0 || K <= 0) return 0;
+  const size_t split = w4a16_workspace_size(M, V, K, x_dtype);
+  if (topk <= 0) return split;
+  return split + round_up((size_t)8 * (size_t)M * (size_t)w4l_topk_parts(V, topk) * (size_t)topk, 256);
+}
+
+int w4a16_lm_head(const void* x, int32_t x_dtype, const uint16_t* embed, float* logits, int64_t M, int64_t V,
+                  int64_t K, float softcap, int32_t topk, float* top_values, int32_t* top_indices, void* workspace,
+                  size_t ws_bytes, void* stream) {
+  static const char* fn = "w4a16_lm_head";
+  clear_err();
+  int rc = check_dims(fn, M, V, K);
+  if (rc) return rc;
+  if (K % 32 != 0) return fail(W4A16_EINVAL_SHAPE, "%s: K=%lld is not a multiple of 32", fn, (long long)K);
+  if (x_dtype != W4A16_DTYPE_BF16 && x_dtype != W4A16_DTYPE_F32)
+    return fail(W4A16_EINVAL_ARG, "%s: unknown x_dtype %d", fn, (int)x_dtype);
+  if (!(softcap >= 0.0f) || softcap > 3.0e38f)
+    return fail(W4A16_EINVAL_ARG, "%s: softcap must be finite and >= 0 (0 = none)", fn);
+  if (topk < 0 || topk > 64) return fail(W4A16_EINVAL_ARG, "%s: topk=%d outside 0..64", fn, (int)topk);
+  if (topk > V) return fail(W4A16_EINVAL_ARG, "%s: topk=%d > V=%lld", fn, (int)topk, (long long)V);
+  if (topk && ((V + 4095) / 4096) * topk > 4096)
+    return fail(W4A16_EINVAL_ARG, "%s: ceil(V / 4096) * topk = %lld exceeds 4096", fn,
+                (long long)(((V + 4095) / 4096) * topk));
+  if (M == 0 || V == 0) return W4A16_OK;
+  if ((rc = check_ptr(logits, "logits", fn))) return rc;
+  if (topk && ((rc = check_ptr(top_values, "top_values", fn)) || (rc = check_ptr(top_indices, "top_indices", fn))))
+    return rc;
+  const size_t need = w4a16_lm_head_workspace_size(M, V, K, x_dtype, topk);
+  if (need) {
+    if (workspace == nullptr || ws_bytes < need)
+      return fail(W4A16_EWORKSPACE, "%s: needs %zu bytes of workspace, got %zu", fn, need,
+                  workspace ? ws_bytes : (size_t)0);
+    if ((rc = check_ptr(workspace, "workspace", fn))) return rc;
+  } else if (workspace != nullptr && !aligned16(workspace)) {
+    return fail(W4A16_EINVAL_PTR, "%s: workspace is not 16-byte aligned", fn);
+  }
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  if (K == 0) {
+    // raw = 0, softcap(0) = 0
+    if ((rc = hip_status(w4l_fill_zero(logits, M * V * 4, st), fn))) return rc;
+  } else {
+    if ((rc = check_ptr(x, "x", fn)) || (rc = check_ptr(embed, "embed", fn))) return rc;
+    const uint16_t* planes = static_cast<const uint16_t*>(x);
+    int nterms = 1;
+    if (x_dtype == W4A16_DTYPE_F32) {
+      uint16_t* split = static_cast<uint16_t*>(workspace);
+      if ((rc = hip_status(w4l_split3(static_cast<const float*>(x), split, M * K, st), fn))) return rc;
+      planes = split;
+      nterms = 3;
+    }
+    const int mc = w4l_head_rows(K, nterms);
+    if (mc == 0) return fail(W4A16_EINVAL_SHAPE, "%s: K=%lld has no launch plan", fn, (long long)K);
+    // chunks of mc rows: rows [m0, m0 + mc) of each plane (planes are M * K halves apart)
+    for (int64_t m0 = 0; m0 < M; m0 += mc) {
+      const int64_t mm = M - m0 < mc ? M - m0 : mc;
+      if ((rc = hip_status(w4l_head_logits(planes + m0 * K, M * K, nterms, embed, logits + m0 * V, mm, V, K, softcap,
+                                           st), fn)))
+        return rc;
+    }
+  }
+  if (topk == 0) return W4A16_OK;
+  uint64_t* cand = reinterpret_cast<uint64_t*>(static_cast<char*>(workspace) + w4a16_workspace_size(M, V, K, x_dtype));
+  return hip_status(w4l_topk(logits, M, V, topk, cand, top_values, top_indices, st), fn);
+}
+
 }  // extern "C"

@@ -70,3 +70,15 @@ hipError_t w4l_fill_zero(void* p, int64_t bytes, hipStream_t st);
 hipError_t w4l_linear(const uint16_t* x_planes, int nterms, const int32_t* pk, const uint16_t* sc,
                       void* y, int y_f32, int64_t M, int64_t N, int64_t K, int32_t group,
                       hipStream_t st);
+
+// lm_head (w4a16_head.hip): f32 logits of a bf16 [V, K] embedding with the
+// softcap applied, for up to w4l_head_rows(K, nterms) rows of x per launch
+// (0 when K is not a multiple of 32), and the deterministic top-k over them
+// (w4l_topk_parts(V, k) * k candidate keys of scratch per row).
+int w4l_head_rows(int64_t K, int nterms);
+// x_planes: nterms planes of [M][K] bf16, xplane halves apart
+hipError_t w4l_head_logits(const uint16_t* x_planes, int64_t xplane, int nterms, const uint16_t* e, float* logits,
+                           int64_t M, int64_t V, int64_t K, float cap, hipStream_t st);
+int64_t w4l_topk_parts(int64_t V, int k);
+hipError_t w4l_topk(const float* logits, int64_t M, int64_t V, int k, uint64_t* cand, float* values,
+                    int32_t* indices, hipStream_t st);

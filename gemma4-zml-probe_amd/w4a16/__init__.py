@@ -12,6 +12,8 @@ Host-side mirror of the reference's W4 brick interface
                           y = x . dequantW4(pk, sc)^T with fp32 accumulation
   gate_up_gelu(x, gate, up)  the MLP front half, zml_runner/engine.zig:653:
                           h = gelu_tanh(x . Wg^T) * (x . Wu^T) in one call
+  lm_head(x, embed)       the decode head, engine.zig:765-766 + gemma4_g12auto.zig:1532:
+                          logits = cap * tanh((x . embed^T) / cap) and their topK
 
 Tensors are torch tensors on the GPU; torch is only the device-memory and
 stream plumbing.  Every call goes through libw4a16.so on the current torch
@@ -39,7 +41,7 @@ GROUP = 32
 # Every symbol include/w4a16.h declares.
 EXPORTS = ("w4a16_version", "w4a16_last_error", "w4a16_unpack", "w4a16_dequant",
            "w4a16_workspace_size", "w4a16_linear", "w4a16_gate_up_workspace_size",
-           "w4a16_gate_up_gelu")
+           "w4a16_gate_up_gelu", "w4a16_lm_head_workspace_size", "w4a16_lm_head")
 GATE_UP_BF16_DOTS = 1
 
 
@@ -83,6 +85,10 @@ def lib() -> ctypes.CDLL:
         L.w4a16_gate_up_gelu.argtypes = [P, I32, P, P, P, P, P, I32, I64, I64, I64, I32, I32, P,
                                          ctypes.c_size_t, P]
         L.w4a16_gate_up_gelu.restype = ctypes.c_int
+        L.w4a16_lm_head_workspace_size.argtypes = [I64, I64, I64, I32, I32]
+        L.w4a16_lm_head_workspace_size.restype = ctypes.c_size_t
+        L.w4a16_lm_head.argtypes = [P, I32, P, P, I64, I64, I64, ctypes.c_float, I32, P, P, P, ctypes.c_size_t, P]
+        L.w4a16_lm_head.restype = ctypes.c_int
         _lib = L
     return _lib
 
@@ -102,6 +108,10 @@ def workspace_size(M: int, N: int, K: int, x_dtype: int = DTYPE_BF16) -> int:
 
 def gate_up_workspace_size(M: int, F: int, K: int, x_dtype: int = DTYPE_BF16) -> int:
     return int(lib().w4a16_gate_up_workspace_size(M, F, K, x_dtype))
+
+
+def lm_head_workspace_size(M: int, V: int, K: int, x_dtype: int = DTYPE_BF16, topk: int = 0) -> int:
+    return int(lib().w4a16_lm_head_workspace_size(M, V, K, x_dtype, topk))
 
 
 # ------------------------------------------------------------ torch-facing API
@@ -253,6 +263,47 @@ def gate_up_gelu(x, gate: "W4Lin", up: "W4Lin", out_dtype=None, bf16_dots: bool 
                                    up.sc.data_ptr(), out.data_ptr(), h_dtype, M, F, K, gate.group,
                                    GATE_UP_BF16_DOTS if bf16_dots else 0, ws_ptr, ws_bytes, _stream_ptr(x)))
     return out
+
+
+def lm_head(x, embed, softcap: float = 30.0, topk: int = 5, logits=None, workspace=None):
+    """The decode head (engine.zig:765-766) and its topK (gemma4_g12auto.zig:1532).
+
+    x bf16 or f32 [..., K]; embed bf16 [V, K] (the tied embedding).  Returns
+    (logits f32 [..., V], values f32 [..., topk], indices int32 [..., topk]) with
+    logits = softcap * tanh((x . embed^T) / softcap) (softcap = 0: no cap); the top-k are
+    descending, equal values in ascending index order.  topk = 0 returns only logits."""
+    torch = _torch()
+    _dev_check(x, embed)
+    if x.dtype not in (torch.bfloat16, torch.float32):
+        raise W4A16Error(EINVAL_ARG, "x must be bf16 or f32")
+    if embed.dtype != torch.bfloat16 or embed.dim() != 2:
+        raise W4A16Error(EINVAL_ARG, "embed must be a 2-D bf16 tensor [V, K]")
+    V, K = embed.shape
+    if x.shape[-1] != K:
+        raise W4A16Error(EINVAL_SHAPE, f"x last dim {x.shape[-1]} != K {K}")
+    lead = tuple(x.shape[:-1])
+    M = 1
+    for d in lead:
+        M *= d
+    x_dtype = DTYPE_BF16 if x.dtype == torch.bfloat16 else DTYPE_F32
+    if logits is None:
+        logits = torch.empty(lead + (V,), dtype=torch.float32, device=x.device)
+    else:
+        _dev_check(logits)
+        if logits.dtype != torch.float32 or logits.numel() != M * V:
+            raise W4A16Error(EINVAL_SHAPE, f"logits must be f32 with {M * V} elements")
+    values = torch.empty(lead + (topk,), dtype=torch.float32, device=x.device) if topk else None
+    indices = torch.empty(lead + (topk,), dtype=torch.int32, device=x.device) if topk else None
+    ws_need = lm_head_workspace_size(M, V, K, x_dtype, topk)
+    ws_ptr, ws_bytes = None, 0
+    if ws_need:
+        if workspace is None:
+            workspace = torch.empty(ws_need, dtype=torch.uint8, device=x.device)
+        ws_ptr, ws_bytes = workspace.data_ptr(), workspace.numel() * workspace.element_size()
+    check(lib().w4a16_lm_head(x.data_ptr(), x_dtype, embed.data_ptr(), logits.data_ptr(), M, V, K,
+                              float(softcap), topk, values.data_ptr() if topk else None,
+                              indices.data_ptr() if topk else None, ws_ptr, ws_bytes, _stream_ptr(x)))
+    return logits, values, indices
 
 
 class W4Lin:

@@ -161,6 +161,35 @@ int w4a16_gate_up_gelu(const void *x, int32_t x_dtype,
                        int64_t M, int64_t F, int64_t K, int32_t group,
                        int32_t flags, void *workspace, size_t ws_bytes, void *stream);
 
+/*
+ * Bytes of device workspace w4a16_lm_head needs: the f32-activation split of
+ * w4a16_workspace_size (x_dtype F32) plus 8 * M * ceil(V / S) * topk bytes of
+ * top-k candidates, S = 1024 when ceil(V / 1024) * topk <= 4096 and 4096
+ * otherwise (0 when topk is 0), rounded up to 256.
+ */
+size_t w4a16_lm_head_workspace_size(int64_t M, int64_t V, int64_t K, int32_t x_dtype, int32_t topk);
+
+/*
+ * The lm_head of the decode step (zml_runner/engine.zig:765-766) and its topK
+ * (zml_runner/gemma4_g12auto.zig:1532):
+ *     raw[M, V]    = x[M, K] . embed[V, K]^T   (the tied bf16 embedding, f32 accumulate:
+ *                                               dotPrec(prec.head, compute, ...) with fam = null)
+ *     logits[M, V] = cap * tanh(raw / cap)     (softcapPrec, engine.zig:193-195; cap = 0: raw)
+ *     top_values[M, topk], top_indices[M, topk]: the topk largest logits of each row,
+ *                    descending; equal values in ascending index order; NaN counts as larger
+ *                    than +inf.  NaN logits are written as the quiet NaN 0x7FC00000.
+ *   x_dtype   W4A16_DTYPE_BF16 or W4A16_DTYPE_F32 (carried exactly, as in w4a16_linear).
+ *   embed     bf16 [V, K], row-major; K % 32 == 0.
+ *   logits    f32 [M, V] output (the step returns it alongside the top-k).
+ *   topk      0..64 with topk <= V and ceil(V / 4096) * topk <= 4096; 0 skips the top-k
+ *             (top_values / top_indices may then be NULL).
+ * The kernels read embed once per 4 rows of x (2 with f32 x): the decode head, M = 1.
+ */
+int w4a16_lm_head(const void *x, int32_t x_dtype, const uint16_t *embed, float *logits,
+                  int64_t M, int64_t V, int64_t K, float softcap, int32_t topk,
+                  float *top_values, int32_t *top_indices,
+                  void *workspace, size_t ws_bytes, void *stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -19,7 +19,13 @@ Reference functions restated (file:line in TheCause/gemma4-zml-probe):
   gate_up_gelu  the MLP front half, zml_runner/engine.zig:653:
                 dot(xff, gate).gelu().mul(dot(xff, up)), gating gelu(gate) * up
                 (PLANNING.md:345), dots through dotPrec (engine.zig:530-533)
-Pins of the last two (tests/test_oracle.py): gelu_tanh against torch's independent
+  softcap       softcapPrec, zml_runner/engine.zig:193-195: raw.scale(1/cap).tanh().scale(cap)
+  topk          logits.topK(.voc, K), zml_runner/gemma4_g12auto.zig:1532: descending; ties in
+                ascending index order and every NaN above +inf (totalOrder of +NaN), which ZML leaves to
+                its sort (parity of tie order unpinned: the reference's own topK test uses
+                distinct values, gemma4_bbatch.zig:766-824)
+  lm_head       engine.zig:765-766: dotPrec(head, last_hidden, embed_tokens) then softcap
+Pins of gelu_tanh / gate_up_gelu (tests/test_oracle.py): gelu_tanh against torch's independent
 gelu(approximate="tanh") in float64, against the defining tanh formula in 400-digit
 decimal arithmetic on the negative tail (where float tanh forms cancel), the odd-part
 identity gelu(x) - gelu(-x) = x, the limits and the closed-form values at 0 and 1;
@@ -204,6 +210,43 @@ def gate_up_gelu(x: np.ndarray, pk_g: np.ndarray, sc_g: np.ndarray, pk_u: np.nda
         ur = bf16_to_f32(round_bf16(u.astype(np.float32))).astype(np.float64)
         return gelu_tanh(gr) * ur, g, u, mg, mu
     return gelu_tanh(g) * u, g, u, mg, mu
+
+
+def softcap(raw, cap: float) -> np.ndarray:
+    """cap * tanh(raw / cap) in float64 (cap = 0: raw unchanged)."""
+    raw = np.asarray(raw, dtype=np.float64)
+    return cap * np.tanh(raw / cap) if cap > 0 else raw
+
+
+def total_order_key(v: np.ndarray) -> np.ndarray:
+    """f32 values -> uint32 keys in IEEE totalOrder (-inf < ... < -0 < +0 < ... < +inf < NaN),
+    every NaN taken as the canonical quiet NaN 0x7FC00000."""
+    v = np.ascontiguousarray(v, dtype=np.float32)
+    u = np.where(np.isnan(v), np.uint32(0x7FC00000), v.view(np.uint32)).astype(np.uint32)
+    return np.where(u & 0x80000000, ~u, u | 0x80000000).astype(np.uint32)
+
+
+def topk(logits: np.ndarray, k: int):
+    """Per row: the k largest f32 values in totalOrder, descending, ties by ascending index.
+    Returns (values f32 [M, k], indices int32 [M, k])."""
+    lg = np.ascontiguousarray(logits, dtype=np.float32)
+    M, V = lg.shape
+    keys = total_order_key(lg)
+    idx = np.empty((M, k), dtype=np.int32)
+    for m in range(M):
+        order = np.lexsort((np.arange(V), -keys[m].astype(np.int64)))
+        idx[m] = order[:k]
+    return np.take_along_axis(lg, idx.astype(np.int64), axis=1), idx
+
+
+def lm_head(x: np.ndarray, embed: np.ndarray, cap: float):
+    """float64 logits softcap(x . embed^T) and the error-bound magnitudes sum |x||e|;
+    x bf16 (uint16) or float32 [M, K], embed bf16 (uint16) [V, K]."""
+    if np.asarray(x).dtype == np.float32:
+        raw, mag = matmul_f32x(x, embed, f64=True)
+    else:
+        raw, mag = matmul_f64(x, embed)
+    return softcap(raw, cap), raw, mag
 
 
 def is_nan_bf16(h: np.ndarray) -> np.ndarray:

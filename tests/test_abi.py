@@ -176,3 +176,36 @@ def test_gate_up_workspace_size(L, M, F, K, xd, fused):
     else:
         assert n >= split + 8 * M * F
     assert L.w4a16_gate_up_workspace_size(0, F, K, xd) == 0
+
+
+def _lm(L, x=A, xd=0, e=A, lg=A, M=1, V=1000, K=256, cap=30.0, k=5, tv=A, ti=A, ws=A, wsb=1 << 20):
+    return L.w4a16_lm_head(x, xd, e, lg, M, V, K, cap, k, tv, ti, ws, wsb, None)
+
+
+def test_lm_head_validation(L):
+    assert _lm(L, M=-1) == w4a16.EINVAL_SHAPE
+    assert _lm(L, K=48) == w4a16.EINVAL_SHAPE              # K % 32
+    assert _lm(L, xd=2) == w4a16.EINVAL_ARG
+    assert _lm(L, cap=-1.0) == w4a16.EINVAL_ARG
+    assert _lm(L, cap=float("nan")) == w4a16.EINVAL_ARG
+    assert _lm(L, cap=float("inf")) == w4a16.EINVAL_ARG
+    assert _lm(L, k=65) == w4a16.EINVAL_ARG
+    assert _lm(L, k=-1) == w4a16.EINVAL_ARG
+    assert _lm(L, V=3, k=4) == w4a16.EINVAL_ARG           # topk > V
+    assert _lm(L, V=4096 * 65, k=64) == w4a16.EINVAL_ARG  # 65 slices * 64 candidates > 4096
+    assert _lm(L, lg=None) == w4a16.EINVAL_PTR
+    assert _lm(L, tv=MIS) == w4a16.EINVAL_PTR
+    assert _lm(L, ti=None) == w4a16.EINVAL_PTR
+    assert _lm(L, ws=None, wsb=0) == w4a16.EWORKSPACE      # top-k candidates need workspace
+    assert _lm(L, ws=A, wsb=64) == w4a16.EWORKSPACE
+    assert _lm(L, M=0, x=None, e=None, lg=None, tv=None, ti=None, ws=None, wsb=0) == 0
+    assert L.w4a16_last_error().decode() == ""
+
+
+def test_lm_head_workspace_size(L):
+    assert L.w4a16_lm_head_workspace_size(1, 262144, 3840, w4a16.DTYPE_BF16, 0) == 0
+    n = L.w4a16_lm_head_workspace_size(1, 262144, 3840, w4a16.DTYPE_BF16, 5)
+    assert n == 10240  # 256 slices of 1024 x 5 candidates x 8 B
+    assert L.w4a16_lm_head_workspace_size(1, 262144, 3840, w4a16.DTYPE_BF16, 64) == 64 * 64 * 8  # 4096-slices
+    split = L.w4a16_workspace_size(2, 262144, 3840, w4a16.DTYPE_F32)
+    assert L.w4a16_lm_head_workspace_size(2, 262144, 3840, w4a16.DTYPE_F32, 5) == split + 20480

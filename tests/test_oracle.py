@@ -352,3 +352,34 @@ def test_gate_up_gelu_bf16_dots_rounds_both_dots():
     assert np.max(np.abs(h - ref.numpy())) <= 1e-12 * max(1.0, float(np.max(np.abs(h))))
     h_plain = o.gate_up_gelu(x, pk_g, sc_g, pk_u, sc_u)[0]
     assert np.max(np.abs(h - h_plain)) > 0
+
+
+# ------------------------------------------------------------------ lm_head: softcap and topK
+# engine.zig:193-195,765-766; gemma4_g12auto.zig:1532
+
+def test_softcap_matches_torch_and_closed_forms():
+    x = np.linspace(-200, 200, 40001)
+    ref = (30.0 * torch.tanh(torch.from_numpy(x) / 30.0)).numpy()
+    assert np.max(np.abs(o.softcap(x, 30.0) - ref)) <= 1e-13
+    assert np.all(np.abs(o.softcap(x, 30.0)) < 30.0)
+    assert np.allclose(o.softcap(-x, 30.0), -o.softcap(x, 30.0), rtol=0, atol=0)
+    small = np.array([1e-6, -3e-4])
+    assert np.allclose(o.softcap(small, 30.0), small, rtol=1e-9)
+    assert np.array_equal(o.softcap(x, 0.0), x)
+
+
+def test_topk_matches_torch_on_distinct_values():
+    rng = np.random.default_rng(17)
+    lg = rng.standard_normal((3, 5000)).astype(np.float32)
+    v, i = o.topk(lg, 7)
+    tv, ti = torch.topk(torch.from_numpy(lg), 7, dim=1, sorted=True)
+    assert np.array_equal(i, ti.numpy()) and np.array_equal(v, tv.numpy())
+
+
+def test_topk_tie_and_nan_order():
+    neg_nan = np.array([0xFFC00000], dtype=np.uint32).view(np.float32)[0]
+    lg = np.array([[1.0, 3.0, 3.0, np.nan, -np.inf, 3.0, np.inf, -0.0, 0.0, neg_nan]], dtype=np.float32)
+    v, i = o.topk(lg, 10)
+    # every NaN first (ties by index), +inf, equal values ascending, +0 above -0
+    assert i[0].tolist() == [3, 9, 6, 1, 2, 5, 0, 8, 7, 4]
+    assert np.isnan(v[0, 0]) and np.isnan(v[0, 1]) and v[0, 2] == np.inf
