@@ -149,6 +149,59 @@ int w4a16_linear(const void* x, int32_t x_dtype, const int32_t* pk, const uint16
   return hip_status(w4l_linear(planes, nterms, pk, sc, y, y_f32, M, N, K, group, st), fn);
 }
 
+int w4a16_linear_group(const void* x, int32_t x_dtype, int32_t n, const int32_t* const* pk,
+                       const uint16_t* const* sc, void* const* y, const int64_t* N, int32_t y_dtype, int64_t M,
+                       int64_t K, int32_t group, int32_t flags, void* workspace, size_t ws_bytes, void* stream) {
+  static const char* fn = "w4a16_linear_group";
+  clear_err();
+  if (n < 1 || n > 4) return fail(W4A16_EINVAL_ARG, "%s: n=%d outside 1..4", fn, (int)n);
+  if (pk == nullptr || sc == nullptr || y == nullptr || N == nullptr)
+    return fail(W4A16_EINVAL_PTR, "%s: pk, sc, y and N must be arrays of n entries", fn);
+  int rc;
+  for (int j = 0; j < n; ++j)
+    if ((rc = check_dims(fn, M, N[j], K))) return rc;
+  if ((rc = check_group(fn, K, group))) return rc;
+  if (x_dtype != W4A16_DTYPE_BF16 && x_dtype != W4A16_DTYPE_F32)
+    return fail(W4A16_EINVAL_ARG, "%s: unknown x_dtype %d", fn, (int)x_dtype);
+  if (y_dtype != W4A16_DTYPE_BF16 && y_dtype != W4A16_DTYPE_F32)
+    return fail(W4A16_EINVAL_ARG, "%s: unknown y_dtype %d", fn, (int)y_dtype);
+  if (flags != 0) return fail(W4A16_EINVAL_ARG, "%s: unknown flags 0x%x", fn, (unsigned)flags);
+  if (M == 0) return W4A16_OK;
+  for (int j = 0; j < n; ++j)
+    if (N[j] && (rc = check_ptr(y[j], "y[j]", fn))) return rc;
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  const int y_f32 = y_dtype == W4A16_DTYPE_F32;
+  if (K == 0) {
+    for (int j = 0; j < n; ++j)
+      if (N[j] && (rc = hip_status(w4l_fill_zero(y[j], M * N[j] * (y_f32 ? 4 : 2), st), fn))) return rc;
+    return W4A16_OK;
+  }
+  if ((rc = check_ptr(x, "x", fn))) return rc;
+  for (int j = 0; j < n; ++j)
+    if (N[j] && ((rc = check_ptr(pk[j], "pk[j]", fn)) || (rc = check_ptr(sc[j], "sc[j]", fn)))) return rc;
+  const uint16_t* planes = static_cast<const uint16_t*>(x);
+  int nterms = 1;
+  if (x_dtype == W4A16_DTYPE_F32) {
+    const size_t need = w4a16_workspace_size(M, 0, K, x_dtype);
+    if (workspace == nullptr || ws_bytes < need)
+      return fail(W4A16_EWORKSPACE, "%s: f32 activations need %zu bytes of workspace, got %zu", fn, need,
+                  workspace ? ws_bytes : (size_t)0);
+    if ((rc = check_ptr(workspace, "workspace", fn))) return rc;
+    uint16_t* split = static_cast<uint16_t*>(workspace);
+    if ((rc = hip_status(w4l_split3(static_cast<const float*>(x), split, M * K, st), fn))) return rc;
+    planes = split;
+    nterms = 3;
+  } else if (workspace != nullptr && !aligned16(workspace)) {
+    return fail(W4A16_EINVAL_PTR, "%s: workspace is not 16-byte aligned", fn);
+  }
+  if (w4l_group_fused(M, K, nterms))
+    return hip_status(w4l_gemv_group(planes, nterms, n, pk, sc, y, N, y_f32, M, K, group, st), fn);
+  for (int j = 0; j < n; ++j)
+    if (N[j] && (rc = hip_status(w4l_linear(planes, nterms, pk[j], sc[j], y[j], y_f32, M, N[j], K, group, st), fn)))
+      return rc;
+  return W4A16_OK;
+}
+
 size_t w4a16_gate_up_workspace_size(int64_t M, int64_t F, int64_t K, int32_t x_dtype) {
   if (M <= 0 || F <= 0 || K <= 0) return 0;
   const size_t split = w4a16_workspace_size(M, F, K, x_dtype);

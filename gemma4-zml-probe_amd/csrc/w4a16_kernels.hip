@@ -388,7 +388,35 @@ struct GemvArgs {
   const uint16_t* sc2;
   int pair_f;
   int bf16_dots;
+  // weight group (gemv_fast_kernel, TPW = 1): nmat > 1 linears that share x;
+  // matrix j owns tiles [tile0[j], tile0[j + 1]) of the grid.
+  int nmat;
+  const uint32_t* gpk[4];
+  const uint16_t* gsc[4];
+  void* gy[4];
+  int gN[4];
+  int tile0[4];
 };
+
+// Matrix of a weight group that owns tile t (uniform across the workgroup);
+// selects rather than indexing, so the arguments stay in scalar registers.
+struct GroupSel {
+  const uint32_t* pk;
+  const uint16_t* sc;
+  void* y;
+  int N;
+  int tile0;
+};
+__device__ __forceinline__ GroupSel group_select(const GemvArgs& a, int t) {
+  GroupSel g{a.pk, a.sc, a.y, a.N, 0};
+  if (a.nmat > 1) {
+    g = GroupSel{a.gpk[0], a.gsc[0], a.gy[0], a.gN[0], a.tile0[0]};
+    if (a.nmat > 1 && t >= a.tile0[1]) g = GroupSel{a.gpk[1], a.gsc[1], a.gy[1], a.gN[1], a.tile0[1]};
+    if (a.nmat > 2 && t >= a.tile0[2]) g = GroupSel{a.gpk[2], a.gsc[2], a.gy[2], a.gN[2], a.tile0[2]};
+    if (a.nmat > 3 && t >= a.tile0[3]) g = GroupSel{a.gpk[3], a.gsc[3], a.gy[3], a.gN[3], a.tile0[3]};
+  }
+  return g;
+}
 
 // NT: bf16 x planes (1, or 3 for f32 x).  KFULL: K % GSTEP == 0 (no partial
 // step).  G32: group == 32 (scale index == 32-column chunk index).
@@ -529,7 +557,11 @@ __global__ void __launch_bounds__(1024) gemv_fast_kernel(GemvArgs a) {
   const int r = lane & 15;
   const int c = lane >> 4;
   const int s0 = wave * NST;
-  const int ntiles = (a.N + 15) >> 4;
+  // the block's matrix (a weight group's member, or the single weight) and its first tile
+  const GroupSel gs = group_select(a, (int)blockIdx.x * TPW);
+  const int N = gs.N;
+  const int bt = (int)blockIdx.x * TPW - gs.tile0;
+  const int ntiles = (N + 15) >> 4;
 
   // 1. x loads (this thread's share), unconditional
   const int nvec = (NT * a.M * a.K) >> 3;
@@ -547,10 +579,10 @@ __global__ void __launch_bounds__(1024) gemv_fast_kernel(GemvArgs a) {
   uint32_t sv[TPW][NST];
 #pragma unroll
   for (int tp = 0; tp < TPW; ++tp) {
-    const int tile = min((int)blockIdx.x * TPW + tp, ntiles - 1);
+    const int tile = min(bt + tp, ntiles - 1);
     const uint32_t* pkrow;
     const uint16_t* scrow;
-    weight_row(a.pk, a.sc, a.pk2, a.sc2, a.pair_f, tile * 16 + r, a.N, a.K, a.groups_per_row, pkrow, scrow);
+    weight_row(gs.pk, gs.sc, a.pk2, a.sc2, a.pair_f, tile * 16 + r, N, a.K, a.groups_per_row, pkrow, scrow);
 #pragma unroll
     for (int i = 0; i < NST; ++i) {
       const int g0 = ((s0 + i) * 4 + c) * VPL;
@@ -610,10 +642,10 @@ __global__ void __launch_bounds__(1024) gemv_fast_kernel(GemvArgs a) {
   __syncthreads();
   if ((int)threadIdx.x < 16 * 4 * TPW) {
     const int tp = threadIdx.x >> 6, m = (threadIdx.x >> 4) & 3, rr = threadIdx.x & 15;
-    const int n = ((int)blockIdx.x * TPW + tp) * 16 + rr;
+    const int n = (bt + tp) * 16 + rr;
     if (a.pair_f) {
       // gate row rr < 8 of the tile and its up row rr + 8
-      const int f = (((int)blockIdx.x * TPW + tp) << 3) + rr;
+      const int f = ((bt + tp) << 3) + rr;
       if (rr < 8 && m < a.M && f < a.pair_f) {
         float g = 0.f, u = 0.f;
         for (int w = 0; w < nwaves; ++w) {
@@ -622,11 +654,11 @@ __global__ void __launch_bounds__(1024) gemv_fast_kernel(GemvArgs a) {
         }
         store_gelu_mul(a.y, a.y_f32, a.bf16_dots, (int64_t)m * a.pair_f + f, g, u);
       }
-    } else if (m < a.M && n < a.N) {
+    } else if (m < a.M && n < N) {
       float v = 0.f;
       for (int w = 0; w < nwaves; ++w) v += red[((tp * nwaves + w) * 4 + m) * 16 + rr];
-      if (a.y_f32) reinterpret_cast<float*>(a.y)[(int64_t)m * a.N + n] = v;
-      else reinterpret_cast<uint16_t*>(a.y)[(int64_t)m * a.N + n] = (uint16_t)f32_to_bf16_rne(v);
+      if (a.y_f32) reinterpret_cast<float*>(gs.y)[(int64_t)m * N + n] = v;
+      else reinterpret_cast<uint16_t*>(gs.y)[(int64_t)m * N + n] = (uint16_t)f32_to_bf16_rne(v);
     }
   }
 }
@@ -1317,6 +1349,47 @@ bool w4l_gemv_stream_plan(int64_t M, int64_t N, int64_t K, int nterms, int* w_ou
   return true;
 }
 
+// Launch of gemv_fast_kernel for a filled GemvArgs: the template arguments
+// follow the plan (x planes, steps per wave, x vectors per thread, tiles per
+// workgroup, group 32).
+static hipError_t gemv_fast_launch(const w4k::GemvArgs& a, int nterms, int nst, int waves, int xpt, int tpw,
+                                   int nblocks, bool g32, hipStream_t st) {
+  const size_t lds = (size_t)nterms * a.M * a.K * 2 + (size_t)tpw * waves * 4 * 16 * 4;
+  const dim3 grid((unsigned)nblocks), block(64 * waves);
+#define W4_FAST(NT_, NST_, XPT_, TPW_)                                                                          \
+  do {                                                                                                          \
+    if (g32) hipLaunchKernelGGL((w4k::gemv_fast_kernel<NT_, NST_, XPT_, TPW_, true>), grid, block, lds, st, a); \
+    else hipLaunchKernelGGL((w4k::gemv_fast_kernel<NT_, NST_, XPT_, TPW_, false>), grid, block, lds, st, a);    \
+  } while (0)
+#define W4_FAST_T(NT_, NST_, XPT_)                        \
+  do {                                                    \
+    if (tpw == 2) W4_FAST(NT_, NST_, XPT_, 2);            \
+    else W4_FAST(NT_, NST_, XPT_, 1);                     \
+  } while (0)
+#define W4_FAST_X(NT_, NST_)                    \
+  switch (xpt) {                                \
+    case 1: W4_FAST_T(NT_, NST_, 1); break;     \
+    case 2: W4_FAST_T(NT_, NST_, 2); break;     \
+    case 4: W4_FAST_T(NT_, NST_, 4); break;     \
+    default: W4_FAST_T(NT_, NST_, 8); break;    \
+  }
+#define W4_FAST_N(NT_)                         \
+  switch (nst) {                               \
+    case 1: W4_FAST_X(NT_, 1); break;          \
+    case 2: W4_FAST_X(NT_, 2); break;          \
+    case 3: W4_FAST_X(NT_, 3); break;          \
+    case 4: W4_FAST_X(NT_, 4); break;          \
+    case 5: W4_FAST_X(NT_, 5); break;          \
+    default: W4_FAST_X(NT_, 6); break;         \
+  }
+  if (nterms == 1) { W4_FAST_N(1) } else { W4_FAST_N(3) }
+#undef W4_FAST_N
+#undef W4_FAST_X
+#undef W4_FAST_T
+#undef W4_FAST
+  return hipGetLastError();
+}
+
 hipError_t w4l_gemv(const uint16_t* x_planes, int nterms, const int32_t* pk, const uint16_t* sc,
                     void* y, int y_f32, int64_t M, int64_t N, int64_t K, int32_t group,
                     hipStream_t st, const W4Pair* pair) {
@@ -1389,41 +1462,7 @@ hipError_t w4l_gemv(const uint16_t* x_planes, int nterms, const int32_t* pk, con
         a.bf16_dots = pair->bf16_dots;
       }
       const int64_t tiles = (N + 15) / 16;
-      const size_t lds = (size_t)nterms * M * K * 2 + (size_t)tpw * waves * 4 * 16 * 4;
-      const dim3 grid((unsigned)((tiles + tpw - 1) / tpw)), block(64 * waves);
-      const bool g32 = group == 32;
-#define W4_FAST(NT_, NST_, XPT_, TPW_)                                                                          \
-  do {                                                                                                          \
-    if (g32) hipLaunchKernelGGL((w4k::gemv_fast_kernel<NT_, NST_, XPT_, TPW_, true>), grid, block, lds, st, a); \
-    else hipLaunchKernelGGL((w4k::gemv_fast_kernel<NT_, NST_, XPT_, TPW_, false>), grid, block, lds, st, a);    \
-  } while (0)
-#define W4_FAST_T(NT_, NST_, XPT_)                        \
-  do {                                                    \
-    if (tpw == 2) W4_FAST(NT_, NST_, XPT_, 2);            \
-    else W4_FAST(NT_, NST_, XPT_, 1);                     \
-  } while (0)
-#define W4_FAST_X(NT_, NST_)                    \
-  switch (xpt) {                                \
-    case 1: W4_FAST_T(NT_, NST_, 1); break;     \
-    case 2: W4_FAST_T(NT_, NST_, 2); break;     \
-    case 4: W4_FAST_T(NT_, NST_, 4); break;     \
-    default: W4_FAST_T(NT_, NST_, 8); break;    \
-  }
-#define W4_FAST_N(NT_)                         \
-  switch (nst) {                               \
-    case 1: W4_FAST_X(NT_, 1); break;          \
-    case 2: W4_FAST_X(NT_, 2); break;          \
-    case 3: W4_FAST_X(NT_, 3); break;          \
-    case 4: W4_FAST_X(NT_, 4); break;          \
-    case 5: W4_FAST_X(NT_, 5); break;          \
-    default: W4_FAST_X(NT_, 6); break;         \
-  }
-      if (nterms == 1) { W4_FAST_N(1) } else { W4_FAST_N(3) }
-#undef W4_FAST_N
-#undef W4_FAST_X
-#undef W4_FAST_T
-#undef W4_FAST
-      return hipGetLastError();
+      return gemv_fast_launch(a, nterms, nst, waves, xpt, tpw, (int)((tiles + tpw - 1) / tpw), group == 32, st);
     }
   }
   if (pair) return hipErrorInvalidValue;
@@ -1649,4 +1688,42 @@ hipError_t w4l_gelu_mul(const float* g, const float* u, void* h, int h_f32, int 
   hipLaunchKernelGGL(w4k::gelu_mul_kernel, dim3(grid_for(n, block)), dim3(block), 0, st, g, u, h, h_f32, bf16_dots,
                      n);
   return hipGetLastError();
+}
+
+bool w4l_group_fused(int64_t M, int64_t K, int nterms) {
+  int nst, waves, xpt, tpw;
+  return w4l_gemv_ok(M, K, nterms) && w4l_gemv_fast_plan(M, 16, K, nterms, &nst, &waves, &xpt, &tpw);
+}
+
+hipError_t w4l_gemv_group(const uint16_t* x_planes, int nterms, int n, const int32_t* const* pk,
+                          const uint16_t* const* sc, void* const* y, const int64_t* N, int y_f32, int64_t M, int64_t K,
+                          int32_t group, hipStream_t st) {
+  int nst, waves, xpt, tpw;
+  if (n < 1 || n > 4 || !w4l_gemv_ok(M, K, nterms) || !w4l_gemv_fast_plan(M, 16, K, nterms, &nst, &waves, &xpt, &tpw))
+    return hipErrorInvalidValue;
+  w4k::GemvArgs a{};
+  a.x = x_planes;
+  a.M = (int)M;
+  a.K = (int)K;
+  a.group_chunks = group / 32;
+  a.groups_per_row = (int)(K / group);
+  a.y_f32 = y_f32;
+  a.steps = (int)(K / w4k::GSTEP);
+  a.nmat = n;
+  int64_t tiles = 0;
+  for (int j = 0; j < n; ++j) {
+    a.gpk[j] = reinterpret_cast<const uint32_t*>(pk[j]);
+    a.gsc[j] = sc[j];
+    a.gy[j] = y[j];
+    a.gN[j] = (int)N[j];
+    a.tile0[j] = (int)tiles;
+    tiles += (N[j] + 15) / 16;
+  }
+  // a matrix with N = 0 owns no tiles; the single-matrix fields stay those of matrix 0
+  a.pk = a.gpk[0];
+  a.sc = a.gsc[0];
+  a.y = a.gy[0];
+  a.N = a.gN[0];
+  if (tiles == 0) return hipSuccess;
+  return gemv_fast_launch(a, nterms, nst, waves, xpt, 1, (int)tiles, group == 32, st);
 }

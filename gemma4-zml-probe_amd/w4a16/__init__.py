@@ -41,7 +41,7 @@ GROUP = 32
 # Every symbol include/w4a16.h declares.
 EXPORTS = ("w4a16_version", "w4a16_last_error", "w4a16_unpack", "w4a16_dequant",
            "w4a16_workspace_size", "w4a16_linear", "w4a16_gate_up_workspace_size",
-           "w4a16_gate_up_gelu", "w4a16_lm_head_workspace_size", "w4a16_lm_head")
+           "w4a16_gate_up_gelu", "w4a16_lm_head_workspace_size", "w4a16_lm_head", "w4a16_linear_group")
 GATE_UP_BF16_DOTS = 1
 
 
@@ -89,6 +89,8 @@ def lib() -> ctypes.CDLL:
         L.w4a16_lm_head_workspace_size.restype = ctypes.c_size_t
         L.w4a16_lm_head.argtypes = [P, I32, P, P, I64, I64, I64, ctypes.c_float, I32, P, P, P, ctypes.c_size_t, P]
         L.w4a16_lm_head.restype = ctypes.c_int
+        L.w4a16_linear_group.argtypes = [P, I32, I32, P, P, P, P, I32, I64, I64, I32, I32, P, ctypes.c_size_t, P]
+        L.w4a16_linear_group.restype = ctypes.c_int
         _lib = L
     return _lib
 
@@ -206,6 +208,53 @@ def linear(x, pk, sc, out_dtype=None, group: int = GROUP, out=None, workspace=No
     check(lib().w4a16_linear(x.data_ptr(), x_dtype, pk.data_ptr(), sc.data_ptr(), out.data_ptr(),
                              y_dtype, M, N, K, group, 0, ws_ptr, ws_bytes, _stream_ptr(x)))
     return out
+
+
+def linear_group(x, lins, out_dtype=None, outs=None, workspace=None):
+    """[x . lin.toW()^T for lin in lins]: 1 to 4 linears that read the same x (q, k, v at
+    engine.zig:552,571,583), one launch at decode.  Each output equals linear(x, lin)."""
+    torch = _torch()
+    if not 1 <= len(lins) <= 4:
+        raise W4A16Error(EINVAL_ARG, "linear_group takes 1 to 4 linears")
+    _dev_check(x, *[t for lin in lins for t in (lin.pk, lin.sc)])
+    if x.dtype not in (torch.bfloat16, torch.float32):
+        raise W4A16Error(EINVAL_ARG, "x must be bf16 or f32")
+    K = lins[0].in_features
+    group = lins[0].group
+    for lin in lins:
+        if lin.in_features != K or lin.group != group:
+            raise W4A16Error(EINVAL_SHAPE, "every linear of a group has the same K and group")
+        if lin.sc.shape[0] != lin.out_features or lin.sc.shape[1] * group != K:
+            raise W4A16Error(EINVAL_SHAPE, f"sc shape {tuple(lin.sc.shape)} does not match pk / group {group}")
+    if x.shape[-1] != K:
+        raise W4A16Error(EINVAL_SHAPE, f"x last dim {x.shape[-1]} != K {K}")
+    lead = tuple(x.shape[:-1])
+    M = 1
+    for d in lead:
+        M *= d
+    if out_dtype is None:
+        out_dtype = x.dtype if outs is None else outs[0].dtype
+    if outs is None:
+        outs = [torch.empty(lead + (lin.out_features,), dtype=out_dtype, device=x.device) for lin in lins]
+    for o_, lin in zip(outs, lins):
+        _dev_check(o_)
+        if o_.dtype != out_dtype or o_.numel() != M * lin.out_features:
+            raise W4A16Error(EINVAL_SHAPE, "outs must match the linears' [M, N] and one dtype")
+    x_dtype = DTYPE_BF16 if x.dtype == torch.bfloat16 else DTYPE_F32
+    ws_need = workspace_size(M, 0, K, x_dtype)
+    ws_ptr, ws_bytes = None, 0
+    if ws_need:
+        if workspace is None:
+            workspace = torch.empty(ws_need, dtype=torch.uint8, device=x.device)
+        ws_ptr, ws_bytes = workspace.data_ptr(), workspace.numel() * workspace.element_size()
+    n = len(lins)
+    arr = lambda vals: (ctypes.c_void_p * n)(*vals)
+    Ns = (ctypes.c_int64 * n)(*[lin.out_features for lin in lins])
+    check(lib().w4a16_linear_group(x.data_ptr(), x_dtype, n, arr([lin.pk.data_ptr() for lin in lins]),
+                                   arr([lin.sc.data_ptr() for lin in lins]), arr([o_.data_ptr() for o_ in outs]), Ns,
+                                   DTYPE_BF16 if out_dtype == torch.bfloat16 else DTYPE_F32, M, K, group, 0,
+                                   ws_ptr, ws_bytes, _stream_ptr(x)))
+    return outs
 
 
 def gate_up_gelu(x, gate: "W4Lin", up: "W4Lin", out_dtype=None, bf16_dots: bool = False, out=None,

@@ -116,6 +116,21 @@ int w4a16_linear(const void *x, int32_t x_dtype,
                  int64_t M, int64_t N, int64_t K, int32_t group,
                  int32_t flags, void *workspace, size_t ws_bytes, void *stream);
 
+/*
+ * Several linears that read the same activations, y_j[M, N_j] = x[M, K] .
+ * dequantW4(pk_j, sc_j)^T for j < n (1 <= n <= 4): q, k and v of a layer, which all
+ * take the normed hidden h0 (zml_runner/engine.zig:552,571,583).  Each y_j is
+ * exactly what w4a16_linear gives for that weight; at decode (M <= 4) the n
+ * linears run as one launch, otherwise one launch each.  pk, sc, y and N are
+ * host arrays of n entries; every weight has K columns and the same group.
+ * Workspace as w4a16_linear (w4a16_workspace_size(M, 0, K, x_dtype)).
+ */
+int w4a16_linear_group(const void *x, int32_t x_dtype, int32_t n,
+                       const int32_t *const *pk, const uint16_t *const *sc,
+                       void *const *y, const int64_t *N, int32_t y_dtype,
+                       int64_t M, int64_t K, int32_t group,
+                       int32_t flags, void *workspace, size_t ws_bytes, void *stream);
+
 /* Flags of w4a16_gate_up_gelu. */
 enum {
     /* g and u rounded to bf16 before the activation: the dot outputs of dotPrec

@@ -209,3 +209,28 @@ def test_lm_head_workspace_size(L):
     assert L.w4a16_lm_head_workspace_size(1, 262144, 3840, w4a16.DTYPE_BF16, 64) == 64 * 64 * 8  # 4096-slices
     split = L.w4a16_workspace_size(2, 262144, 3840, w4a16.DTYPE_F32)
     assert L.w4a16_lm_head_workspace_size(2, 262144, 3840, w4a16.DTYPE_F32, 5) == split + 20480
+
+
+def test_linear_group_validation(L):
+    arr = lambda *v: (ctypes.c_void_p * len(v))(*v)
+    Ns = (ctypes.c_int64 * 2)(16, 32)
+
+    def grp(n=2, pk=None, sc=None, y=None, N=Ns, M=1, K=64, xd=0, yd=0, flags=0, x=A):
+        pk = arr(A, A) if pk is None else pk
+        sc = arr(A, A) if sc is None else sc
+        y = arr(A, A) if y is None else y
+        return L.w4a16_linear_group(x, xd, n, pk, sc, y, N, yd, M, K, 32, flags, None, 0, None)
+
+    assert grp(n=0) == w4a16.EINVAL_ARG
+    assert grp(n=5) == w4a16.EINVAL_ARG
+    assert L.w4a16_linear_group(A, 0, 2, None, arr(A, A), arr(A, A), Ns, 0, 1, 64, 32, 0, None, 0, None) \
+        == w4a16.EINVAL_PTR
+    assert grp(N=(ctypes.c_int64 * 2)(16, -1)) == w4a16.EINVAL_SHAPE
+    assert grp(K=80) == w4a16.EINVAL_SHAPE
+    assert grp(yd=3) == w4a16.EINVAL_ARG
+    assert grp(flags=1) == w4a16.EINVAL_ARG
+    assert grp(y=arr(A, MIS)) == w4a16.EINVAL_PTR
+    assert grp(pk=arr(A, None)) == w4a16.EINVAL_PTR
+    assert grp(xd=1) == w4a16.EWORKSPACE
+    assert grp(M=0, x=None) == 0
+    assert L.w4a16_last_error().decode() == ""

@@ -486,3 +486,32 @@ def test_prefill_kernel_small_m(M, N, K, monkeypatch):
     yb = gpu_linear(x, pk, sc, "bf16")
     _, mag = o.matmul_f64(x, w)
     check_bf16(yb, ref32, mag, K)
+
+
+@pytest.mark.parametrize("M,Ns,K,x_f32,out", [
+    (1, (4096, 2048, 2048), 3840, False, "bf16"),   # 12B q, k, v at decode: one launch
+    (3, (17, 0, 33, 5), 512, False, "f32"),        # ragged N, an empty member
+    (2, (64, 48), 1536, True, "f32"),               # f32 x
+    (20, (40, 24, 16), 256, False, "bf16"),         # above decode: one launch per weight
+])
+def test_linear_group_equals_single_linears(M, Ns, K, x_f32, out):
+    """w4a16_linear_group (q, k, v read the same x, engine.zig:552,571,583): every output
+    equals w4a16_linear of that weight bit for bit (same per-row arithmetic), and the
+    first member is checked against the oracle."""
+    say(f"linear_group M={M} Ns={Ns} K={K} x_f32={x_f32} out={out}")
+    ws = [o.synth_weights(n, K, 60 + j)[1:] for j, n in enumerate(Ns)]
+    x_np = o.synth_x(M, K, 61)
+    if x_f32:
+        x_np = (o.bf16_to_f32(x_np) * np.float32(1.0 + 2.0 ** -10)).astype(np.float32)
+    x = dev(x_np) if x_f32 else dev_u16(x_np)
+    lins = [w4a16.W4Lin(dev(pk), dev_u16(sc)) for pk, sc in ws]
+    odt = torch.float32 if out == "f32" else torch.bfloat16
+    ys = w4a16.linear_group(x, lins, out_dtype=odt)
+    singles = [w4a16.linear(x, lin.pk, lin.sc, out_dtype=odt) for lin in lins]
+    torch.cuda.synchronize()
+    for y, y1 in zip(ys, singles):
+        assert torch.equal(y.view(torch.int32 if out == "f32" else torch.int16),
+                           y1.view(torch.int32 if out == "f32" else torch.int16))
+    if Ns[0] and out == "f32":
+        w = o.dequant(*ws[0])
+        check_f32(ys[0].cpu().numpy(), x_np, w, K, x_f32=x_f32)
