@@ -103,11 +103,22 @@ int w4a16_dequant(const int32_t* pk, const uint16_t* sc, uint16_t* w, int64_t N,
   return hip_status(w4l_dequant(pk, sc, w, N, K, group, static_cast<hipStream_t>(stream)), fn);
 }
 
+namespace {
+// f32 activations: their three bf16 planes (required workspace)
+size_t x_split_bytes(int64_t M, int64_t K, int32_t x_dtype) {
+  if (M <= 0 || K <= 0 || x_dtype != W4A16_DTYPE_F32) return 0;
+  return round_up((size_t)(3 * 2) * (size_t)M * (size_t)K, 256);
+}
+// bf16 activations, 4 < M <= 64: the split-K partial sums (optional workspace;
+// without it the call takes the one-pass skinny route)
+size_t splitk_bytes(int64_t M, int64_t N, int64_t K, int32_t x_dtype) {
+  if (M <= 0 || N <= 0 || K <= 0 || x_dtype != W4A16_DTYPE_BF16) return 0;
+  return round_up(w4l_splitk_bytes(M, N, K, 1), 256);
+}
+}  // namespace
+
 size_t w4a16_workspace_size(int64_t M, int64_t N, int64_t K, int32_t x_dtype) {
-  (void)N;
-  if (M <= 0 || K <= 0) return 0;
-  if (x_dtype == W4A16_DTYPE_F32) return round_up((size_t)(3 * 2) * (size_t)M * (size_t)K, 256);
-  return 0;
+  return x_split_bytes(M, K, x_dtype) + splitk_bytes(M, N, K, x_dtype);
 }
 
 int w4a16_linear(const void* x, int32_t x_dtype, const int32_t* pk, const uint16_t* sc, void* y,
@@ -134,7 +145,7 @@ int w4a16_linear(const void* x, int32_t x_dtype, const int32_t* pk, const uint16
   const uint16_t* planes = static_cast<const uint16_t*>(x);
   int nterms = 1;
   if (x_dtype == W4A16_DTYPE_F32) {
-    const size_t need = w4a16_workspace_size(M, N, K, x_dtype);
+    const size_t need = x_split_bytes(M, K, x_dtype);
     if (workspace == nullptr || ws_bytes < need)
       return fail(W4A16_EWORKSPACE, "%s: f32 activations need %zu bytes of workspace, got %zu", fn,
                   need, workspace ? ws_bytes : (size_t)0);
@@ -145,6 +156,12 @@ int w4a16_linear(const void* x, int32_t x_dtype, const int32_t* pk, const uint16
     nterms = 3;
   } else if (workspace != nullptr && !aligned16(workspace)) {
     return fail(W4A16_EINVAL_PTR, "%s: workspace is not 16-byte aligned", fn);
+  } else if (workspace != nullptr) {
+    const size_t sk = splitk_bytes(M, N, K, x_dtype);
+    if (sk && ws_bytes >= sk)
+      return hip_status(w4l_splitk(planes, pk, sc, y, y_f32, M, N, K, group, st, nullptr,
+                                   static_cast<float*>(workspace)),
+                        fn);
   }
   return hip_status(w4l_linear(planes, nterms, pk, sc, y, y_f32, M, N, K, group, st), fn);
 }
@@ -182,7 +199,7 @@ int w4a16_linear_group(const void* x, int32_t x_dtype, int32_t n, const int32_t*
   const uint16_t* planes = static_cast<const uint16_t*>(x);
   int nterms = 1;
   if (x_dtype == W4A16_DTYPE_F32) {
-    const size_t need = w4a16_workspace_size(M, 0, K, x_dtype);
+    const size_t need = x_split_bytes(M, K, x_dtype);
     if (workspace == nullptr || ws_bytes < need)
       return fail(W4A16_EWORKSPACE, "%s: f32 activations need %zu bytes of workspace, got %zu", fn, need,
                   workspace ? ws_bytes : (size_t)0);
@@ -202,12 +219,25 @@ int w4a16_linear_group(const void* x, int32_t x_dtype, int32_t n, const int32_t*
   return W4A16_OK;
 }
 
-size_t w4a16_gate_up_workspace_size(int64_t M, int64_t F, int64_t K, int32_t x_dtype) {
+namespace {
+// workspace a gate/up call cannot do without: the x planes (f32 x) and, for
+// shapes no fused kernel takes, f32 g and u
+size_t gate_up_required(int64_t M, int64_t F, int64_t K, int32_t x_dtype) {
   if (M <= 0 || F <= 0 || K <= 0) return 0;
-  const size_t split = w4a16_workspace_size(M, F, K, x_dtype);
+  const size_t split = x_split_bytes(M, K, x_dtype);
   const int nterms = x_dtype == W4A16_DTYPE_F32 ? 3 : 1;
   if (w4l_gate_up_fused(M, F, K, nterms)) return split;
   return split + 2 * round_up((size_t)4 * (size_t)M * (size_t)F, 256);  // f32 g, then u
+}
+// optional: the split-K partial sums over the 16 * ceil(F / 8) virtual rows
+size_t gate_up_splitk(int64_t M, int64_t F, int64_t K, int32_t x_dtype) {
+  if (M <= 0 || F <= 0 || K <= 0 || F > INT_MAX / 2 - 16) return 0;
+  return splitk_bytes(M, 16 * ((F + 7) / 8), K, x_dtype);
+}
+}  // namespace
+
+size_t w4a16_gate_up_workspace_size(int64_t M, int64_t F, int64_t K, int32_t x_dtype) {
+  return gate_up_required(M, F, K, x_dtype) + gate_up_splitk(M, F, K, x_dtype);
 }
 
 int w4a16_gate_up_gelu(const void* x, int32_t x_dtype, const int32_t* pk_gate, const uint16_t* sc_gate,
@@ -236,7 +266,7 @@ int w4a16_gate_up_gelu(const void* x, int32_t x_dtype, const int32_t* pk_gate, c
       (rc = check_ptr(sc_gate, "sc_gate", fn)) || (rc = check_ptr(pk_up, "pk_up", fn)) ||
       (rc = check_ptr(sc_up, "sc_up", fn)))
     return rc;
-  const size_t need = w4a16_gate_up_workspace_size(M, F, K, x_dtype);
+  const size_t need = gate_up_required(M, F, K, x_dtype);
   if (need) {
     if (workspace == nullptr || ws_bytes < need)
       return fail(W4A16_EWORKSPACE, "%s: this shape needs %zu bytes of workspace, got %zu", fn, need,
@@ -254,13 +284,18 @@ int w4a16_gate_up_gelu(const void* x, int32_t x_dtype, const int32_t* pk_gate, c
     if ((rc = hip_status(w4l_split3(static_cast<const float*>(x), split, M * K, st), fn))) return rc;
     planes = split;
     nterms = 3;
-    ws += w4a16_workspace_size(M, F, K, x_dtype);
+    ws += x_split_bytes(M, K, x_dtype);
   }
   W4Pair pair;
   pair.pk_up = pk_up;
   pair.sc_up = sc_up;
   pair.F = F;
   pair.bf16_dots = (flags & W4A16_GATE_UP_BF16_DOTS) ? 1 : 0;
+  const size_t sk = gate_up_splitk(M, F, K, x_dtype);
+  if (sk && workspace != nullptr && ws_bytes >= sk)
+    return hip_status(w4l_splitk(planes, pk_gate, sc_gate, h, h_f32, M, 0, K, group, st, &pair,
+                                 reinterpret_cast<float*>(ws)),
+                      fn);
   if (w4l_gate_up_fused(M, F, K, nterms))
     return hip_status(w4l_gate_up(planes, nterms, pk_gate, sc_gate, pair, h, h_f32, M, K, group, st), fn);
   // unfused route: g and u in f32 through the workspace, then the activation
@@ -273,7 +308,7 @@ int w4a16_gate_up_gelu(const void* x, int32_t x_dtype, const int32_t* pk_gate, c
 
 size_t w4a16_lm_head_workspace_size(int64_t M, int64_t V, int64_t K, int32_t x_dtype, int32_t topk) {
   if (M <= 0 || V <= 0 || K <= 0) return 0;
-  const size_t split = w4a16_workspace_size(M, V, K, x_dtype);
+  const size_t split = x_split_bytes(M, K, x_dtype);
   if (topk <= 0) return split;
   return split + round_up((size_t)8 * (size_t)M * (size_t)w4l_topk_parts(V, topk) * (size_t)topk, 256);
 }
@@ -333,7 +368,7 @@ int w4a16_lm_head(const void* x, int32_t x_dtype, const uint16_t* embed, float* 
     }
   }
   if (topk == 0) return W4A16_OK;
-  uint64_t* cand = reinterpret_cast<uint64_t*>(static_cast<char*>(workspace) + w4a16_workspace_size(M, V, K, x_dtype));
+  uint64_t* cand = reinterpret_cast<uint64_t*>(static_cast<char*>(workspace) + x_split_bytes(M, K, x_dtype));
   return hip_status(w4l_topk(logits, M, V, topk, cand, top_values, top_indices, st), fn);
 }
 

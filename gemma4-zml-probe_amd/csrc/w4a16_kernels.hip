@@ -1022,8 +1022,12 @@ struct PrefillArgs {
   int group_chunks;
   int groups_per_row;
   int y_f32;
-  int ns;    // K / 64
-  int mblk;  // ceil(M / 256)
+  int ns;    // steps (64 KS columns each) per K part
+  int mblk;  // ceil(M / BM)
+  // split K across workgroups: kq parts of ns steps each; part q of every
+  // output tile goes to part[q][M][N] (f32), which splitk_finalize_kernel sums
+  int kq;
+  float* part;
   // gate/up pair mode, as GemvArgs
   const uint32_t* pk2;
   const uint16_t* sc2;
@@ -1031,17 +1035,30 @@ struct PrefillArgs {
   int bf16_dots;
 };
 
-template <int TN, int P, bool G32, int MB = 8>  // MB: 32-row blocks of x per workgroup
-__global__ void __launch_bounds__(256) prefill_kernel(PrefillArgs a) {
+// Small M (the skinny regime) uses WS waves of W rows and a K split KS: a step
+// covers 64*KS columns, wave (wsub, kh) takes the kh-th 64 of them for its
+// 32*TN rows, and the KS partial sums meet in LDS at the end.  That keeps
+// enough waves in flight when a 64-row x tile leaves few workgroups, while
+// each A fragment still feeds a 32x32x16 MFMA (half the LDS reads per weight
+// of the 16x16x32 form).
+template <int TN, int P, bool G32, int MB = 8, int WS = 4, int KS = 1>  // MB: 32-row blocks of x per workgroup
+__global__ void __launch_bounds__(64 * WS * KS) prefill_kernel(PrefillArgs a) {
+  constexpr int NTH = 64 * WS * KS;
   constexpr int BM = 32 * MB;
-  constexpr int BN = 4 * 32 * TN;
+  constexpr int BN = WS * 32 * TN;
   constexpr int XPAD = 8;
-  __shared__ __attribute__((aligned(16))) uint16_t xs[2][BM][64 + XPAD];
+  __shared__ __attribute__((aligned(16))) uint16_t xs[2][KS][BM][64 + XPAD];
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int wsub = wave % WS, kh = wave / WS;
   const int l32 = lane & 31, h = lane >> 5;
-  const int m0 = ((int)blockIdx.x % a.mblk) * BM;
-  const int nw0 = ((int)blockIdx.x / a.mblk) * BN + wave * 32 * TN;
+  // workgroup b: K part b % kq (consecutive workgroups, on different XCDs, share
+  // the W tile), then x block, then W tile
+  const int kpart = (int)blockIdx.x % a.kq;
+  const int bt = (int)blockIdx.x / a.kq;
+  const int m0 = (bt % a.mblk) * BM;
+  const int nw0 = (bt / a.mblk) * BN + wsub * 32 * TN;
+  const int sbase = kpart * a.ns;  // first step of this part
 
   const uint32_t* pkrow[TN];
   const uint16_t* scrow[TN];
@@ -1055,20 +1072,23 @@ __global__ void __launch_bounds__(256) prefill_kernel(PrefillArgs a) {
     constexpr int slot = decltype(slot_c)::value;
 #pragma unroll
     for (int t = 0; t < TN; ++t) {
-      const int g = 2 * s + h;
+      const int g = 2 * ((sbase + s) * KS + kh) + h;
       wv[slot][t] = *reinterpret_cast<const uint4*>(pkrow[t] + 4 * g);
       sv[slot][t] = scrow[t][G32 ? g : g / a.group_chunks];
     }
   };
-  constexpr int XV = BM * 8 / 256;  // 16-byte vectors of the [BM][64] step per thread
+  // 16-byte vectors of the [BM][64 KS] step per thread; vector v is row
+  // v / (8 KS), columns 8 (v % (8 KS)) .. +8 of the step, LDS tile (v % (8 KS)) / 8
+  constexpr int XV = BM * 8 * KS / NTH;
+  static_assert(XV >= 1 && XV * NTH == BM * 8 * KS, "x step must split evenly over the threads");
   typedef uint32_t xvec_t __attribute__((ext_vector_type(4 * XV)));
   auto xload = [&](xvec_t& xr, int s) __attribute__((always_inline)) {
 #pragma unroll
     for (int i = 0; i < XV; ++i) {
-      const int v = (int)threadIdx.x + 256 * i;
-      const int row = v >> 3, col = (v & 7) * 8;
+      const int v = (int)threadIdx.x + NTH * i;
+      const int row = v / (8 * KS), col = (v % (8 * KS)) * 8;
       const int m = min(m0 + row, a.M - 1);
-      const u32x4 t = *reinterpret_cast<const u32x4*>(a.x + (int64_t)m * a.K + s * 64 + col);
+      const u32x4 t = *reinterpret_cast<const u32x4*>(a.x + (int64_t)m * a.K + (sbase + s) * 64 * KS + col);
       xr[4 * i] = t[0];
       xr[4 * i + 1] = t[1];
       xr[4 * i + 2] = t[2];
@@ -1078,9 +1098,10 @@ __global__ void __launch_bounds__(256) prefill_kernel(PrefillArgs a) {
   auto xstore = [&](const xvec_t& xr, int buf) __attribute__((always_inline)) {
 #pragma unroll
     for (int i = 0; i < XV; ++i) {
-      const int v = (int)threadIdx.x + 256 * i;
-      const int row = v >> 3, col = (v & 7) * 8;
-      *reinterpret_cast<u32x4*>(&xs[buf][row][col]) = u32x4{xr[4 * i], xr[4 * i + 1], xr[4 * i + 2], xr[4 * i + 3]};
+      const int v = (int)threadIdx.x + NTH * i;
+      const int row = v / (8 * KS), u = v % (8 * KS);
+      *reinterpret_cast<u32x4*>(&xs[buf][u >> 3][row][(u & 7) * 8]) =
+          u32x4{xr[4 * i], xr[4 * i + 1], xr[4 * i + 2], xr[4 * i + 3]};
     }
   };
 
@@ -1113,7 +1134,7 @@ __global__ void __launch_bounds__(256) prefill_kernel(PrefillArgs a) {
     }
     bf16x8 xa[2][MB];
 #pragma unroll
-    for (int i = 0; i < MB; ++i) xa[0][i] = *reinterpret_cast<const bf16x8*>(&xs[buf][32 * i + l32][32 * h]);
+    for (int i = 0; i < MB; ++i) xa[0][i] = *reinterpret_cast<const bf16x8*>(&xs[buf][kh][32 * i + l32][32 * h]);
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
       // A fragments of step j+1 go out before the MFMAs of step j; the scheduling
@@ -1122,7 +1143,7 @@ __global__ void __launch_bounds__(256) prefill_kernel(PrefillArgs a) {
       if (j < 3) {
 #pragma unroll
         for (int i = 0; i < MB; ++i)
-          xa[(j + 1) & 1][i] = *reinterpret_cast<const bf16x8*>(&xs[buf][32 * i + l32][32 * h + 8 * (j + 1)]);
+          xa[(j + 1) & 1][i] = *reinterpret_cast<const bf16x8*>(&xs[buf][kh][32 * i + l32][32 * h + 8 * (j + 1)]);
       }
       __builtin_amdgcn_sched_barrier(0);
       bf16x8 bb[TN];
@@ -1162,6 +1183,56 @@ __global__ void __launch_bounds__(256) prefill_kernel(PrefillArgs a) {
   // the last MFMAs must finish before their AGPRs are read (16-pass MFMA: >= 18 wait states)
   asm volatile("s_nop 7\n\ts_nop 7\n\ts_nop 7\n\ts_nop 7" ::: "memory");
 
+  if constexpr (KS > 1) {
+    // waves kh > 0 hand their partial sums to kh = 0 through the x tiles (idle:
+    // every iteration ended with a barrier)
+    constexpr int NE = MB * TN * 16;
+    static_assert((KS - 1) * WS * NE * 64 * 4 <= (int)sizeof(xs), "reduction buffer fits in the x tiles");
+    float* red = reinterpret_cast<float*>(&xs[0][0][0][0]);
+    auto at = [&](int q, int e) { return ((q * WS + wsub) * NE + e) * 64 + lane; };
+    if (kh > 0) {
+      static_for<0, MB>([&](auto i_c) __attribute__((always_inline)) {
+        static_for<0, TN>([&](auto t_c) __attribute__((always_inline)) {
+          constexpr int i = decltype(i_c)::value, t = decltype(t_c)::value;
+#pragma unroll
+          for (int e = 0; e < 16; ++e) red[at(kh - 1, (i * TN + t) * 16 + e)] = acc[i][t][e];
+        });
+      });
+    }
+    __syncthreads();
+    if (kh > 0) return;
+    static_for<0, MB>([&](auto i_c) __attribute__((always_inline)) {
+      static_for<0, TN>([&](auto t_c) __attribute__((always_inline)) {
+        constexpr int i = decltype(i_c)::value, t = decltype(t_c)::value;
+#pragma unroll
+        for (int q = 0; q < KS - 1; ++q)
+#pragma unroll
+          for (int e = 0; e < 16; ++e) acc[i][t][e] += red[at(q, (i * TN + t) * 16 + e)];
+      });
+    });
+  }
+
+  if (a.kq > 1) {
+    // split K: this part's sums, every row m < M of every row n < N (the pair
+    // layout is resolved by the finalize kernel)
+    static_for<0, TN>([&](auto t_c) __attribute__((always_inline)) {
+      constexpr int t = decltype(t_c)::value;
+      const int n = nw0 + 32 * t + l32;
+      if (n < a.N) {
+        float* pp = a.part + (int64_t)kpart * a.M * a.N + n;
+        static_for<0, MB>([&](auto i_c) __attribute__((always_inline)) {
+          constexpr int i = decltype(i_c)::value;
+#pragma unroll
+          for (int e = 0; e < 16; ++e) {
+            const int m = m0 + 32 * i + 8 * (e >> 2) + 4 * h + (e & 3);
+            if (m < a.M) pp[(int64_t)m * a.N] = acc[i][t][e];
+          }
+        });
+      }
+    });
+    return;
+  }
+
   static_for<0, TN>([&](auto t_c) __attribute__((always_inline)) {
     constexpr int t = decltype(t_c)::value;
     const int n = nw0 + 32 * t + l32;
@@ -1198,6 +1269,37 @@ __global__ void __launch_bounds__(256) prefill_kernel(PrefillArgs a) {
       });
     }
   });
+}
+
+// Split-K combine: y[m][n] = sum over q < kq of part[q][m][n] (f32 or bf16 out),
+// or in gate/up pair mode (pair_f = F) h[m][f] = gelu(g) * u with g and u the
+// sums of virtual rows ((f >> 3) << 4) | (f & 7) and that | 8.  The parts are
+// added in q order, so the result does not depend on scheduling.
+__global__ void __launch_bounds__(256) splitk_finalize_kernel(const float* __restrict__ part, int kq, int M, int N,
+                                                              void* y, int y_f32, int pair_f, int bf16_dots) {
+  const int cols = pair_f ? pair_f : N;
+  const int64_t total = (int64_t)M * cols;
+  const int64_t plane = (int64_t)M * N;
+  const int64_t stride = (int64_t)gridDim.x * blockDim.x;
+  for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < total; i += stride) {
+    const int m = (int)(i / cols), col = (int)(i % cols);
+    if (pair_f) {
+      const int vg = ((col >> 3) << 4) | (col & 7);
+      const float* pg = part + (int64_t)m * N + vg;
+      float g = 0.f, u = 0.f;
+      for (int q = 0; q < kq; ++q) {
+        g += pg[q * plane];
+        u += pg[q * plane + 8];
+      }
+      store_gelu_mul(y, y_f32, bf16_dots, i, g, u);
+    } else {
+      const float* pv = part + (int64_t)m * N + col;
+      float v = 0.f;
+      for (int q = 0; q < kq; ++q) v += pv[q * plane];
+      if (y_f32) reinterpret_cast<float*>(y)[i] = v;
+      else reinterpret_cast<uint16_t*>(y)[i] = (uint16_t)f32_to_bf16_rne(v);
+    }
+  }
 }
 
 // h = gelu(g) * u elementwise over f32 g, u: the combine step of the unfused
@@ -1583,10 +1685,43 @@ hipError_t w4l_prefill(const uint16_t* x, const int32_t* pk, const uint16_t* sc,
   a.groups_per_row = (int)(K / group);
   a.y_f32 = y_f32;
   a.ns = (int)(K / 64);
-  // x rows per workgroup: 64 / 128 / 256 (MB = 2 / 4 / 8 blocks of 32), the smallest that
-  // holds M, so small M pays no MFMAs on padding rows
-  const int mb = M <= 64 ? 2 : M <= 128 ? 4 : 8;
+  a.kq = 1;
+  // x rows per workgroup: 32 / 64 / 128 / 256 (MB = 1 / 2 / 4 / 8 blocks of 32), the
+  // smallest that holds M, so small M pays no MFMAs on padding rows
+  const int mb = M <= 32 ? 1 : M <= 64 ? 2 : M <= 128 ? 4 : 8;
   a.mblk = (int)((M + 32 * mb - 1) / (32 * mb));
+  if (mb <= 2) {
+    // the skinny regime: WS waves of W rows x a K split KS (tuning overrides
+    // W4A16_PF_WS=<2|4>, W4A16_PF_KS=<1|2|4>)
+    int ws = 4, ks = 2;
+    if (const char* e = getenv("W4A16_PF_WS")) ws = atoi(e) == 2 ? 2 : 4;
+    if (const char* e = getenv("W4A16_PF_KS")) ks = atoi(e);
+    if (ks != 1 && ks != 2 && ks != 4) ks = 2;
+    if (ws == 4 && ks == 4) ks = 2;
+    while (ks > 1 && K % (64 * ks) != 0) ks /= 2;
+    a.ns = (int)(K / (64 * ks));
+    const int bn = ws * 32;
+    const dim3 grid((unsigned)(((N + bn - 1) / bn) * a.mblk)), block(64 * ws * ks);
+    const bool g32 = group == 32;
+#define W4_PFS(MB_, WS_, KS_)                                                                                \
+  do {                                                                                                       \
+    if (g32) hipLaunchKernelGGL((w4k::prefill_kernel<1, 4, true, MB_, WS_, KS_>), grid, block, 0, st, a);   \
+    else hipLaunchKernelGGL((w4k::prefill_kernel<1, 4, false, MB_, WS_, KS_>), grid, block, 0, st, a);      \
+  } while (0)
+#define W4_PFS_M(WS_, KS_)          \
+  do {                              \
+    if (mb == 1) W4_PFS(1, WS_, KS_); \
+    else W4_PFS(2, WS_, KS_);         \
+  } while (0)
+    if (ws == 4 && ks == 1) W4_PFS_M(4, 1);
+    else if (ws == 4) W4_PFS_M(4, 2);
+    else if (ks == 1) W4_PFS_M(2, 1);
+    else if (ks == 2) W4_PFS_M(2, 2);
+    else W4_PFS_M(2, 4);
+#undef W4_PFS_M
+#undef W4_PFS
+    return hipGetLastError();
+  }
   // two W blocks of 32 rows per wave when that still leaves two workgroups per CU
   const bool tn2 = mb == 8 && ((N + 255) / 256) * a.mblk >= 512;
   const int bn = tn2 ? 256 : 128;
@@ -1605,13 +1740,101 @@ hipError_t w4l_prefill(const uint16_t* x, const int32_t* pk, const uint16_t* sc,
   return hipGetLastError();
 }
 
+// Split-K plan for the skinny regime (4 < M <= 64, bf16 x) when the skinny
+// kernel's grid (N / 64 workgroups) cannot fill the GPU: N < 16384 rows, and
+// M > 16 or K >= 8192 (measured on the 12B q/k/v/o/down shapes: at M <= 16 and
+// K = 3840 the one-pass kernel is as fast).  Workgroups of WS waves x 32 W rows
+// (256 rows for M > 32, 128 for M <= 32; x blocks of 64 / 32 rows) and kq K
+// parts, the smallest divisor of K / 64 (<= 16) that gives >= 240 workgroups,
+// else the largest.  Costs kq f32 partial planes and one finalize pass; 12B down
+// at M = 64 goes from 75 to 28 us.  W4A16_SPLITK=0 turns it off and
+// W4A16_PF_KQ=<q> forces the part count (tuning).
+namespace {
+bool splitk_plan(int64_t M, int64_t N, int64_t K, int nterms, int* ws, int* kq, int* mb) {
+  if (nterms != 1 || M <= 4 || M > 64 || K % 64 != 0 || N <= 0 || N >= 16384) return false;
+  if (M <= 16 && K < 8192) return false;
+  if (const char* e = getenv("W4A16_SPLITK"))
+    if (atoi(e) == 0) return false;
+  *mb = M <= 32 ? 1 : 2;
+  *ws = *mb == 2 ? 8 : 4;
+  const int64_t tiles = (N + 32 * *ws - 1) / (32 * *ws);
+  const int64_t steps = K / 64;
+  int q = 0;
+  if (const char* e = getenv("W4A16_PF_KQ")) {
+    const int v = atoi(e);
+    if (v >= 1 && v <= 16 && steps % v == 0) q = v;
+  }
+  for (int c = 2; !q && c <= 16; ++c)
+    if (steps % c == 0 && tiles * c >= 240) q = c;
+  if (!q) {
+    for (int c = 16; c >= 2 && !q; --c)
+      if (steps % c == 0) q = c;
+  }
+  if (q < 2) return false;
+  *kq = q;
+  return true;
+}
+}  // namespace
+
+size_t w4l_splitk_bytes(int64_t M, int64_t N, int64_t K, int nterms) {
+  int ws, kq, mb;
+  if (!splitk_plan(M, N, K, nterms, &ws, &kq, &mb)) return 0;
+  return (size_t)kq * (size_t)M * (size_t)N * sizeof(float);
+}
+
+hipError_t w4l_splitk(const uint16_t* x, const int32_t* pk, const uint16_t* sc, void* y, int y_f32, int64_t M,
+                      int64_t N, int64_t K, int32_t group, hipStream_t st, const W4Pair* pair, float* part) {
+  int ws, kq, mb;
+  const int64_t Nv = pair ? 16 * ((pair->F + 7) / 8) : N;
+  if (!splitk_plan(M, Nv, K, 1, &ws, &kq, &mb)) return hipErrorInvalidValue;
+  w4k::PrefillArgs a{};
+  if (pair) {
+    a.pk2 = reinterpret_cast<const uint32_t*>(pair->pk_up);
+    a.sc2 = pair->sc_up;
+    a.pair_f = (int)pair->F;
+    a.bf16_dots = pair->bf16_dots;
+  }
+  a.x = x;
+  a.pk = reinterpret_cast<const uint32_t*>(pk);
+  a.sc = sc;
+  a.y = y;
+  a.M = (int)M;
+  a.N = (int)Nv;
+  a.K = (int)K;
+  a.group_chunks = group / 32;
+  a.groups_per_row = (int)(K / group);
+  a.y_f32 = y_f32;
+  a.ns = (int)(K / 64 / kq);
+  a.mblk = (int)((M + 32 * mb - 1) / (32 * mb));
+  a.kq = kq;
+  a.part = part;
+  const int bn = 32 * ws;
+  const dim3 grid((unsigned)(((Nv + bn - 1) / bn) * a.mblk * kq)), block(64 * ws);
+  const bool g32 = group == 32;
+#define W4_SKQ(MB_, WS_)                                                                                   \
+  do {                                                                                                     \
+    if (g32) hipLaunchKernelGGL((w4k::prefill_kernel<1, 4, true, MB_, WS_, 1>), grid, block, 0, st, a);   \
+    else hipLaunchKernelGGL((w4k::prefill_kernel<1, 4, false, MB_, WS_, 1>), grid, block, 0, st, a);      \
+  } while (0)
+  if (mb == 2) W4_SKQ(2, 8);
+  else W4_SKQ(1, 4);
+#undef W4_SKQ
+  hipError_t e = hipGetLastError();
+  if (e != hipSuccess) return e;
+  const int64_t outs = M * (pair ? pair->F : N);
+  const int block_f = 256;
+  hipLaunchKernelGGL(w4k::splitk_finalize_kernel, dim3(grid_for(outs, block_f)), dim3(block_f), 0, st, part, kq,
+                     (int)M, (int)Nv, y, y_f32, pair ? (int)pair->F : 0, pair ? pair->bf16_dots : 0);
+  return hipGetLastError();
+}
+
 hipError_t w4l_linear(const uint16_t* x_planes, int nterms, const int32_t* pk, const uint16_t* sc,
                       void* y, int y_f32, int64_t M, int64_t N, int64_t K, int32_t group,
                       hipStream_t st) {
   if (w4l_gemv_ok(M, K, nterms)) return w4l_gemv(x_planes, nterms, pk, sc, y, y_f32, M, N, K, group, st);
   if (w4l_prefill_ok(M, K, nterms)) return w4l_prefill(x_planes, pk, sc, y, y_f32, M, N, K, group, st);
-  // W4A16_PF_SMALL=1: tuning switch, 16 < M <= 64 through the 32x32 kernel with 64 rows of x
-  if (getenv("W4A16_PF_SMALL") && nterms == 1 && M > 16 && K % 64 == 0)
+  // W4A16_PF_SMALL=1: tuning switch, 4 < M <= 64 through the 32x32 kernel
+  if (getenv("W4A16_PF_SMALL") && nterms == 1 && M > 4 && K % 64 == 0)
     return w4l_prefill(x_planes, pk, sc, y, y_f32, M, N, K, group, st);
   if (w4l_skinny_ok(M, K, nterms)) return w4l_skinny(x_planes, pk, sc, y, y_f32, M, N, K, group, st);
   const W4Plan p = w4l_plan(M, N, K, nterms);
@@ -1662,6 +1885,7 @@ PairRoute pair_route(int64_t M, int64_t F, int64_t K, int nterms) {
   if (w4l_gemv_ok(M, K, nterms) && w4l_gemv_fast_plan(M, 16 * ((F + 7) / 8), K, nterms, &nst, &waves, &xpt, &tpw))
     return PAIR_GEMV;
   if (w4l_prefill_ok(M, K, nterms)) return PAIR_PREFILL;
+  if (getenv("W4A16_PF_SMALL") && nterms == 1 && M > 4 && K % 64 == 0) return PAIR_PREFILL;
   if (nterms == 1 && K % 256 == 0) return PAIR_SKINNY;
   return PAIR_NONE;
 }

@@ -78,6 +78,12 @@ hipError_t w4l_fill_zero(void* p, int64_t bytes, hipStream_t st);
 hipError_t w4l_linear(const uint16_t* x_planes, int nterms, const int32_t* pk, const uint16_t* sc,
                       void* y, int y_f32, int64_t M, int64_t N, int64_t K, int32_t group,
                       hipStream_t st);
+// Split-K route of the skinny regime (bf16 x, 4 < M <= 64): bytes of f32 partial
+// sums it needs (0 when the shape does not take it) and the launch (main kernel
+// + finalize); with pair set, N is ignored and the output is h [M, F].
+size_t w4l_splitk_bytes(int64_t M, int64_t N, int64_t K, int nterms);
+hipError_t w4l_splitk(const uint16_t* x, const int32_t* pk, const uint16_t* sc, void* y, int y_f32, int64_t M,
+                      int64_t N, int64_t K, int32_t group, hipStream_t st, const W4Pair* pair, float* part);
 
 // lm_head (w4a16_head.hip): f32 logits of a bf16 [V, K] embedding with the
 // softcap applied, for up to w4l_head_rows(K, nterms) rows of x per launch

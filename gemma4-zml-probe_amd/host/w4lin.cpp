@@ -145,6 +145,39 @@ void gate_up_gelu(const W4Lin& gate, const W4Lin& up, const uint16_t* x, float* 
   gate_up_call(gate, up, x, h, W4A16_DTYPE_F32, m, workspace, ws_bytes, stream, bf16_dots);
 }
 
+void linear_group(const std::vector<W4Lin>& lins, const uint16_t* x, const std::vector<uint16_t*>& ys, int64_t m,
+                  hipStream_t stream) {
+  if (lins.empty() || lins.size() > 4 || ys.size() != lins.size())
+    throw Error(W4A16_EINVAL_ARG, "linear_group: 1 to 4 linears, one output each");
+  const int32_t* pk[4];
+  const uint16_t* sc[4];
+  void* y[4];
+  int64_t n[4];
+  for (size_t j = 0; j < lins.size(); ++j) {
+    if (lins[j].k != lins[0].k || lins[j].group != lins[0].group)
+      throw Error(W4A16_EINVAL_SHAPE, "linear_group: every linear needs the same k and group");
+    pk[j] = lins[j].pk;
+    sc[j] = lins[j].sc;
+    y[j] = ys[j];
+    n[j] = lins[j].n;
+  }
+  check(w4a16_linear_group(x, W4A16_DTYPE_BF16, (int32_t)lins.size(), pk, sc, y, n, W4A16_DTYPE_BF16, m,
+                           lins[0].k, lins[0].group, 0, nullptr, 0, stream),
+        "linear_group");
+}
+
+size_t lm_head_workspace(int64_t m, int64_t v, int64_t k, int topk) {
+  return w4a16_lm_head_workspace_size(m, v, k, W4A16_DTYPE_BF16, topk);
+}
+
+void lm_head(const uint16_t* embed, int64_t v, int64_t k, const uint16_t* x, int64_t m, float softcap, int topk,
+             float* logits, float* top_values, int32_t* top_indices, void* workspace, size_t ws_bytes,
+             hipStream_t stream) {
+  check(w4a16_lm_head(x, W4A16_DTYPE_BF16, embed, logits, m, v, k, softcap, topk, top_values, top_indices, workspace,
+                      ws_bytes, stream),
+        "lm_head");
+}
+
 Census census(const SafeTensorsFile& f) {
   Census c;
   for (const auto& kv : f.tensors()) {

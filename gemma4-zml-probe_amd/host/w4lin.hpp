@@ -92,6 +92,20 @@ void gate_up_gelu(const W4Lin& gate, const W4Lin& up, const uint16_t* x, uint16_
 void gate_up_gelu(const W4Lin& gate, const W4Lin& up, const uint16_t* x, float* h, int64_t m, void* workspace,
                   size_t ws_bytes, hipStream_t stream, bool bf16_dots = false);
 
+// Linears that read the same x (q, k, v at engine.zig:552,571,583): ys[j][m, lins[j].n] =
+// x . lins[j].toW()^T, one launch at decode; 1..4 linears with the same k and group.
+void linear_group(const std::vector<W4Lin>& lins, const uint16_t* x, const std::vector<uint16_t*>& ys, int64_t m,
+                  hipStream_t stream);
+
+// The decode head (engine.zig:765-766) and its topK (gemma4_g12auto.zig:1532): logits[m, v] =
+// softcap * tanh(x . embed^T / softcap) (f32), top-k values (descending, ties by index) and
+// indices.  embed is the tied bf16 [v, k] embedding on the device; workspace of
+// lm_head_workspace(m, v, k, topk) bytes.
+size_t lm_head_workspace(int64_t m, int64_t v, int64_t k, int topk);
+void lm_head(const uint16_t* embed, int64_t v, int64_t k, const uint16_t* x, int64_t m, float softcap, int topk,
+             float* logits, float* top_values, int32_t* top_indices, void* workspace, size_t ws_bytes,
+             hipStream_t stream);
+
 // ---------------------------------------------------------------- checkpoint census
 struct CensusEntry {
   std::string name;  // module name, without ".weight_packed"

@@ -12,6 +12,12 @@
 //       w[n, k] = toW() (bf16) on the GPU.
 //   w4lin_tool mlp <file.safetensors> <gate> <up> <M> <x.bin> <h.bin> [bf16|f32]
 //       h[M, F] = gelu_tanh(x . gate^T) * (x . up^T) on the GPU (engine.zig:653).
+//   w4lin_tool qkv <file.safetensors> <prefix> <j> <M> <x.bin> <out_prefix>
+//       q, k (and v on sliding layers) of layer j as one grouped call (engine.zig:552-583);
+//       writes <out_prefix>.q.bin, .k.bin[, .v.bin] (bf16).
+//   w4lin_tool head <file.safetensors> <embed_name> <M> <x.bin> <softcap> <topk> <out_prefix>
+//       logits (f32) and top-k of the tied-embedding head (engine.zig:765-766);
+//       writes <out_prefix>.logits.bin, .values.bin (f32), .indices.bin (i32).
 #include <hip/hip_runtime.h>
 
 #include <cstdio>
@@ -32,7 +38,9 @@ int usage() {
                "       w4lin_tool layer12 <file> <prefix> <j>\n"
                "       w4lin_tool linear <file> <name> <M> <x.bin> <y.bin> [bf16|f32]\n"
                "       w4lin_tool dequant <file> <name> <w.bin>\n"
-               "       w4lin_tool mlp <file> <gate> <up> <M> <x.bin> <h.bin> [bf16|f32]\n");
+               "       w4lin_tool mlp <file> <gate> <up> <M> <x.bin> <h.bin> [bf16|f32]\n"
+               "       w4lin_tool qkv <file> <prefix> <j> <M> <x.bin> <out_prefix>\n"
+               "       w4lin_tool head <file> <embed_name> <M> <x.bin> <softcap> <topk> <out_prefix>\n");
   return 2;
 }
 
@@ -161,6 +169,74 @@ int cmd_mlp(int argc, char** argv) {
   return 0;
 }
 
+int cmd_qkv(int argc, char** argv) {
+  if (argc < 8) return usage();
+  const int j = std::atoi(argv[4]);
+  const int64_t M = std::atoll(argv[5]);
+  w4::DeviceStore store(argv[2]);
+  const std::string l = std::string(argv[3]) + "." + std::to_string(j) + ".self_attn.";
+  std::vector<std::string> names = {"q_proj", "k_proj"};
+  if (!w4::g12_is_full(j)) names.push_back("v_proj");  // full layers: V = K (g12.zig)
+  std::vector<w4::W4Lin> lins;
+  for (const auto& n : names) lins.push_back(w4::W4Lin::init(store, l + n));
+  const auto x = read_file(argv[6], (size_t)(M * lins[0].k * 2));
+  void* dx = nullptr;
+  hip_ok(hipMalloc(&dx, std::max<size_t>(x.size(), 16)), "hipMalloc x");
+  hip_ok(hipMemcpy(dx, x.data(), x.size(), hipMemcpyHostToDevice), "copy x");
+  std::vector<uint16_t*> ys;
+  for (const auto& lin : lins) {
+    void* p = nullptr;
+    hip_ok(hipMalloc(&p, std::max<size_t>((size_t)(M * lin.n * 2), 16)), "hipMalloc y");
+    ys.push_back(static_cast<uint16_t*>(p));
+  }
+  w4::linear_group(lins, static_cast<const uint16_t*>(dx), ys, M, nullptr);
+  for (size_t i = 0; i < lins.size(); ++i) {
+    std::vector<char> h((size_t)(M * lins[i].n * 2));
+    hip_ok(hipMemcpy(h.data(), ys[i], h.size(), hipMemcpyDeviceToHost), "copy y");
+    write_file(std::string(argv[7]) + "." + names[i].substr(0, 1) + ".bin", h.data(), h.size());
+    (void)hipFree(ys[i]);
+  }
+  (void)hipFree(dx);
+  std::printf("{\"layer\": %d, \"linears\": %zu, \"M\": %lld}\n", j, lins.size(), (long long)M);
+  return 0;
+}
+
+int cmd_head(int argc, char** argv) {
+  if (argc < 9) return usage();
+  const int64_t M = std::atoll(argv[4]);
+  const float cap = (float)std::atof(argv[6]);
+  const int topk = std::atoi(argv[7]);
+  w4::DeviceStore store(argv[2]);
+  const w4::TensorInfo& ti = store.file().info(argv[3]);
+  if (ti.dtype != "BF16" || ti.shape.size() != 2) throw std::runtime_error(std::string(argv[3]) + ": not bf16 [V, K]");
+  const int64_t V = ti.shape[0], K = ti.shape[1];
+  const uint16_t* e = static_cast<const uint16_t*>(store.device(argv[3]));
+  const auto x = read_file(argv[5], (size_t)(M * K * 2));
+  const size_t ws = w4::lm_head_workspace(M, V, K, topk);
+  void *dx = nullptr, *dl = nullptr, *dv = nullptr, *di = nullptr, *dws = nullptr;
+  hip_ok(hipMalloc(&dx, std::max<size_t>(x.size(), 16)), "hipMalloc x");
+  hip_ok(hipMalloc(&dl, std::max<size_t>((size_t)(M * V * 4), 16)), "hipMalloc logits");
+  hip_ok(hipMalloc(&dv, std::max<size_t>((size_t)(M * topk * 4), 16)), "hipMalloc values");
+  hip_ok(hipMalloc(&di, std::max<size_t>((size_t)(M * topk * 4), 16)), "hipMalloc indices");
+  if (ws) hip_ok(hipMalloc(&dws, ws), "hipMalloc workspace");
+  hip_ok(hipMemcpy(dx, x.data(), x.size(), hipMemcpyHostToDevice), "copy x");
+  w4::lm_head(e, V, K, static_cast<const uint16_t*>(dx), M, cap, topk, static_cast<float*>(dl),
+              static_cast<float*>(dv), static_cast<int32_t*>(di), dws, ws, nullptr);
+  const std::string out = argv[8];
+  std::vector<char> b((size_t)(M * V * 4));
+  hip_ok(hipMemcpy(b.data(), dl, b.size(), hipMemcpyDeviceToHost), "copy logits");
+  write_file(out + ".logits.bin", b.data(), b.size());
+  b.resize((size_t)(M * topk * 4));
+  hip_ok(hipMemcpy(b.data(), dv, b.size(), hipMemcpyDeviceToHost), "copy values");
+  write_file(out + ".values.bin", b.data(), b.size());
+  hip_ok(hipMemcpy(b.data(), di, b.size(), hipMemcpyDeviceToHost), "copy indices");
+  write_file(out + ".indices.bin", b.data(), b.size());
+  for (void* p : {dx, dl, dv, di, dws})
+    if (p) (void)hipFree(p);
+  std::printf("{\"V\": %lld, \"K\": %lld, \"M\": %lld, \"topk\": %d}\n", (long long)V, (long long)K, (long long)M, topk);
+  return 0;
+}
+
 int cmd_dequant(int argc, char** argv) {
   if (argc < 5) return usage();
   w4::DeviceStore store(argv[2]);
@@ -187,6 +263,8 @@ int main(int argc, char** argv) {
     if (cmd == "linear") return cmd_linear(argc, argv);
     if (cmd == "dequant") return cmd_dequant(argc, argv);
     if (cmd == "mlp") return cmd_mlp(argc, argv);
+    if (cmd == "qkv") return cmd_qkv(argc, argv);
+    if (cmd == "head") return cmd_head(argc, argv);
     return usage();
   } catch (const w4::Error& e) {
     std::fprintf(stderr, "w4lin_tool: %s (status %d)\n", e.what(), e.status());

@@ -168,7 +168,9 @@ def linear(x, pk, sc, out_dtype=None, group: int = GROUP, out=None, workspace=No
 
     x: bf16 or f32 [..., K] (leading dims flattened to M rows).  out_dtype
     bf16 (default for bf16 x) or f32 (default for f32 x).  f32 activations
-    need workspace (allocated here when not given).
+    need workspace; bf16 activations at 4 < M <= 64 on the smaller 12B rows can
+    use it for the split-K route (allocated here when not given; pass an
+    empty tensor to take the one-pass route instead).
     """
     torch = _torch()
     _dev_check(x, pk, sc)

@@ -29,7 +29,8 @@
  *     host threads on different streams.
  *   - The caller owns every device buffer.  No entry point allocates device
  *     memory.  w4a16_linear takes caller-provided workspace where a shape
- *     needs it (see w4a16_workspace_size).
+ *     needs it, or where it makes a faster route possible (see
+ *     w4a16_workspace_size).
  *   - Device pointers must be 16-byte aligned (pk, sc, x, y, q, w, workspace).
  *     Row strides are the dense ones implied by the shapes; K % group == 0
  *     and group % 32 == 0 are required.
@@ -84,9 +85,17 @@ int w4a16_dequant(const int32_t *pk, const uint16_t *sc, uint16_t *w,
                   int64_t N, int64_t K, int32_t group, void *stream);
 
 /*
- * Bytes of device workspace w4a16_linear needs for (M, N, K, x_dtype).
- * x_dtype = W4A16_DTYPE_F32 needs 6 * M * K bytes (rounded up to 256) to
- * hold the three bf16 terms of x; W4A16_DTYPE_BF16 needs none (0).
+ * Bytes of device workspace w4a16_linear can use for (M, N, K, x_dtype).
+ * x_dtype = W4A16_DTYPE_F32: 6 * M * K bytes (rounded up to 256) to hold the
+ * three bf16 terms of x, required.
+ * x_dtype = W4A16_DTYPE_BF16: nothing is required.  For 4 < M <= 64 on shapes
+ * whose one-pass kernel cannot fill the GPU (N < 16384, K % 64 == 0, and M > 16
+ * or K >= 8192: the 12B q/k/v/o/down rows) it is the size of kq f32 partial
+ * planes, kq * M * N * 4 bytes rounded up to 256 with 2 <= kq <= 16 K parts;
+ * given at least that much, the call splits K across workgroups and adds the
+ * parts in a second launch in a fixed order (deterministic).  With less, or
+ * NULL, it takes the one-pass route; both meet the same fp32 bound.  0
+ * otherwise.
  */
 size_t w4a16_workspace_size(int64_t M, int64_t N, int64_t K, int32_t x_dtype);
 
@@ -107,8 +116,10 @@ size_t w4a16_workspace_size(int64_t M, int64_t N, int64_t K, int32_t x_dtype);
  *            result rounded to nearest even once, as the bf16 dot of the
  *            fam = bf16 flow).
  *   flags    must be 0.
- *   workspace / ws_bytes  at least w4a16_workspace_size(M, N, K, x_dtype)
- *            bytes (NULL / 0 allowed when that is 0); W4A16_EWORKSPACE otherwise.
+ *   workspace / ws_bytes  f32 x: at least the x-planes part of
+ *            w4a16_workspace_size, W4A16_EWORKSPACE otherwise; bf16 x: optional
+ *            (NULL / 0 allowed), the split-K route when ws_bytes reaches
+ *            w4a16_workspace_size(M, N, K, x_dtype).
  */
 int w4a16_linear(const void *x, int32_t x_dtype,
                  const int32_t *pk, const uint16_t *sc,
@@ -139,13 +150,17 @@ enum {
 };
 
 /*
- * Bytes of device workspace w4a16_gate_up_gelu needs for (M, F, K, x_dtype):
- * the f32-activation split of w4a16_workspace_size, plus 2 * 4 * M * F bytes for
- * f32 g and u on shapes that no fused kernel takes (then g and u make a round
- * trip through the workspace).  The second part is 0 when a fused kernel
- * takes the shape: bf16 x with K % 256 == 0 (any M) or with M > 64 and
- * K % 64 == 0 (every Gemma gate/up shape: K = 1536 or 3840); f32 x in the
- * decode GEMV (M <= 4, K % 256 == 0, within its LDS and register limits).
+ * Bytes of device workspace w4a16_gate_up_gelu can use for (M, F, K, x_dtype).
+ * Required: the f32-activation x planes of w4a16_workspace_size, plus
+ * 2 * 4 * M * F bytes for f32 g and u on shapes that no fused kernel takes
+ * (then g and u make a round trip through the workspace).  That second part is
+ * 0 when a fused kernel takes the shape: bf16 x with K % 256 == 0 (any M) or
+ * with M > 64 and K % 64 == 0 (every Gemma gate/up shape: K = 1536 or 3840);
+ * f32 x in the decode GEMV (M <= 4, K % 256 == 0, within its LDS and register
+ * limits).  Optional, added on top: bf16 x at 4 < M <= 64 takes the split-K
+ * route of w4a16_linear over the 16 * ceil(F / 8) interleaved gate/up rows
+ * when that row count is below 16384 (E2B: F = 6144 at M > 16), with the
+ * activation applied when the parts are added.
  */
 size_t w4a16_gate_up_workspace_size(int64_t M, int64_t F, int64_t K, int32_t x_dtype);
 
@@ -167,7 +182,9 @@ size_t w4a16_gate_up_workspace_size(int64_t M, int64_t F, int64_t K, int32_t x_d
  *             once to nearest even).
  *   flags     0 or W4A16_GATE_UP_BF16_DOTS.
  *   group     shared by both weights.
- *   workspace / ws_bytes  at least w4a16_gate_up_workspace_size(M, F, K, x_dtype).
+ *   workspace / ws_bytes  at least the required part of
+ *             w4a16_gate_up_workspace_size (W4A16_EWORKSPACE otherwise); the
+ *             split-K route when it reaches the whole size.
  */
 int w4a16_gate_up_gelu(const void *x, int32_t x_dtype,
                        const int32_t *pk_gate, const uint16_t *sc_gate,

@@ -93,11 +93,49 @@ def test_unpack_dequant_validation(L):
     assert L.w4a16_dequant(None, None, None, 0, 64, 32, None) == 0
 
 
+def splitk_bytes(M, N, K):
+    """Optional split-K workspace of a bf16 linear (partial sums): 4 < M <= 64,
+    N < 16384, K % 64 == 0, and M > 16 or K >= 8192; kq = the smallest divisor
+    q <= 16 of K / 64 with tiles * q >= 240 (tiles of 256 W rows at M > 32, 128
+    below), else the largest divisor <= 16."""
+    if not (4 < M <= 64 and 0 < N < 16384 and K % 64 == 0 and (M > 16 or K >= 8192)):
+        return 0
+    tiles = -(-N // (256 if M > 32 else 128))
+    steps = K // 64
+    divs = [q for q in range(2, 17) if steps % q == 0]
+    if not divs:
+        return 0
+    fill = [q for q in divs if tiles * q >= 240]
+    q = fill[0] if fill else divs[-1]
+    return -(-(q * M * N * 4) // 256) * 256
+
+
 def test_workspace_size(L):
     assert L.w4a16_workspace_size(1, 4096, 3840, w4a16.DTYPE_BF16) == 0
     n = L.w4a16_workspace_size(3, 4096, 3840, w4a16.DTYPE_F32)
     assert n >= 6 * 3 * 3840 and n % 256 == 0
     assert L.w4a16_workspace_size(0, 4096, 3840, w4a16.DTYPE_F32) == 0
+
+
+@pytest.mark.parametrize("M,N,K,expect", [
+    (64, 3840, 15360, 16 * 64 * 3840 * 4),  # 12B down: 15 tiles x 16 parts
+    (8, 3840, 15360, 8 * 8 * 3840 * 4),     # 30 tiles of 128 rows x 8 parts
+    (64, 4096, 3840, 15 * 64 * 4096 * 4),   # 12B q: 16 tiles, 15 | 60 steps
+    (64, 2048, 3840, 15 * 64 * 2048 * 4),   # k/v: no divisor fills, the largest <= 16
+    (32, 12288, 1536, 3 * 32 * 12288 * 4),  # E2B gate/up rows at M = 32
+    (16, 4096, 3840, 0),                    # M <= 16 at K < 8192: one-pass skinny
+    (64, 30720, 3840, 0),                   # the skinny grid fills the GPU
+    (4, 3840, 15360, 0),                    # decode GEMV
+    (65, 3840, 15360, 0),                   # prefill
+    (64, 3840, 15360 + 32, 0),              # K % 64 != 0
+])
+def test_workspace_size_splitk(L, M, N, K, expect):
+    """bf16 x: the optional split-K workspace (a call with less takes the
+    one-pass route); f32 x adds it to nothing (split-K is bf16-only)."""
+    assert splitk_bytes(M, N, K) == expect
+    assert L.w4a16_workspace_size(M, N, K, w4a16.DTYPE_BF16) == expect
+    planes = -(-(6 * M * K) // 256) * 256
+    assert L.w4a16_workspace_size(M, N, K, w4a16.DTYPE_F32) == planes
 
 
 def test_python_wrapper_refuses_cpu_tensors():
@@ -166,15 +204,17 @@ def test_gate_up_gelu_validation(L):
     (2, 24, 96, 0, False),
     (1, 72, 1024, 1, True),        # f32 x in the decode GEMV
     (8, 40, 512, 1, False),        # f32 x above M = 4
+    (32, 6144, 1536, 0, True),     # E2B at M = 32: split-K partials over 12288 virtual rows
 ])
 def test_gate_up_workspace_size(L, M, F, K, xd, fused):
     n = L.w4a16_gate_up_workspace_size(M, F, K, xd)
-    split = L.w4a16_workspace_size(M, F, K, xd)
+    planes = -(-(6 * M * K) // 256) * 256 if xd == 1 else 0
+    extra = splitk_bytes(M, 16 * -(-F // 8), K) if xd == 0 else 0  # over the virtual rows
     assert n % 256 == 0
     if fused:
-        assert n == split
+        assert n == planes + extra
     else:
-        assert n >= split + 8 * M * F
+        assert n >= planes + 8 * M * F
     assert L.w4a16_gate_up_workspace_size(0, F, K, xd) == 0
 
 

@@ -117,9 +117,10 @@ CASES = [
     (1, 15360, 3840, 32, False, True, False),   # 12B gate/up decode
     (4, 70, 3840, 32, False, True, False),      # M = 4 at K = 3840 -> skinny
     (5, 33, 256, 32, False, False, False),      # skinny
-    (17, 9, 512, 32, False, True, False),       # skinny, one real row in the second tile
-    (40, 129, 1280, 32, False, True, True),     # skinny, bf16 dots
-    (64, 200, 768, 128, False, True, False),    # skinny, group 128
+    (17, 9, 512, 32, False, True, False),       # split-K, one real row in the second x block
+    (40, 129, 1280, 32, False, True, True),     # split-K, bf16 dots
+    (64, 200, 768, 128, False, True, False),    # split-K (400 virtual rows), group 128
+    (32, 6144, 1536, 32, False, True, False),   # split-K: E2B gate/up at M = 32
     (65, 50, 64, 32, False, True, False),       # prefill
     (300, 130, 192, 64, False, False, False),   # prefill, h bf16
     (257, 17, 320, 32, False, True, True),      # prefill, bf16 dots
@@ -139,6 +140,23 @@ def test_gate_up_gelu_vs_oracle(M, F, K, group, x_f32, h_f32, bf16_dots):
         x = (o.bf16_to_f32(x) * np.float32(1.0 + 2.0 ** -10)).astype(np.float32)  # not bf16-representable
     h = run_gpu(x, pk_g, sc_g, pk_u, sc_u, group, x_f32, h_f32, bf16_dots)
     check(h, x, pk_g, sc_g, pk_u, sc_u, K, group, h_f32, bf16_dots)
+
+
+@pytest.mark.parametrize("h_f32", [True, False])
+def test_gate_up_gelu_one_pass_without_workspace(h_f32):
+    """E2B gate/up at M = 48: with an empty workspace the call takes the one-pass
+    skinny route instead of split-K; both meet the bound."""
+    M, F, K = 48, 6144, 1536
+    say(f"gate_up_gelu one-pass M={M} F={F} K={K} h_f32={h_f32}")
+    assert w4a16.gate_up_workspace_size(M, F, K, w4a16.DTYPE_BF16) > 0
+    pk_g, sc_g, pk_u, sc_u = weights(F, K, 4600, 32)
+    x = o.synth_x(M, K, 4601)
+    h = w4a16.gate_up_gelu(dev_bf16(x), w4lin(pk_g, sc_g, 32), w4lin(pk_u, sc_u, 32),
+                           out_dtype=torch.float32 if h_f32 else torch.bfloat16,
+                           workspace=torch.empty(0, dtype=torch.uint8, device="cuda"))
+    torch.cuda.synchronize()
+    h = h.cpu().numpy().astype(np.float64) if h_f32 else o.bf16_to_f32(host_u16(h)).astype(np.float64)
+    check(h, x, pk_g, sc_g, pk_u, sc_u, K, 32, h_f32, False)
 
 
 def test_gate_up_gelu_equals_two_linears_at_12b_prefill():

@@ -282,6 +282,36 @@ def test_linear_c4_12b_gateup(M):
     check_head_argmax(y[:, rows], ref32, len(rows))
 
 
+@pytest.mark.parametrize("M,K,N,step", [
+    (64, 15360, 3840, 13),  # 12B down at M = 64: 15 W tiles x 16 K parts
+    (8, 15360, 3840, 13),   # M = 8 at K >= 8192: 32-row x blocks, 8 parts
+    (40, 3840, 2048, 1),    # 12B k/v rows, partial last x block
+    (33, 4096, 1000, 1),    # ragged N (last W tile partial), 64-row x block with one real row in its second half
+    (20, 1536, 300, 1),     # small: K / 64 = 24 steps
+])
+def test_linear_splitk_route(M, K, N, step):
+    """The split-K route (bf16 x, 4 < M <= 64, a skinny grid too small to fill the
+    GPU): the default call (the wrapper allocates the optional workspace) and the
+    one-pass route (no workspace) both meet the stated f32 tolerance against the
+    oracle on every `step`-th row n; bf16 outputs meet the bf16 bound."""
+    say(f"split-K M={M} K={K} N={N}")
+    assert w4a16.workspace_size(M, N, K, w4a16.DTYPE_BF16) > 0
+    _, pk, sc = o.synth_weights(N, K, 1100 + N)
+    x = o.synth_x(M, K, 1200 + M)
+    rows = np.arange(0, N, step)
+    w = o.dequant(pk[rows], sc[rows])
+    ref32 = o.matmul_f32(x, w)
+    xt, pkt, sct = dev_u16(x), dev(pk), dev_u16(sc)
+    for ws in (None, torch.empty(0, dtype=torch.uint8, device="cuda")):
+        y = w4a16.linear(xt, pkt, sct, out_dtype=torch.float32, workspace=ws)
+        torch.cuda.synchronize()
+        check_f32(y.cpu().numpy()[:, rows], x, w, K, ref32)
+    yb = w4a16.linear(xt, pkt, sct, out_dtype=torch.bfloat16)
+    torch.cuda.synchronize()
+    _, mag = o.matmul_f64(x, w)
+    check_bf16(host_u16(yb)[:, rows], ref32, mag, K)
+
+
 @pytest.mark.parametrize("K,N", [(3840, 30720), (15360, 3840)])
 def test_linear_c5_prefill(K, N):
     """M = 2048; oracle on a sample of rows m and n."""

@@ -241,3 +241,72 @@ def test_cpp_gate_up_gelu_on_gpu(tool, tmp_path, M, out):
         h = o.bf16_to_f32(np.fromfile(tmp_path / "h.bin", dtype=np.uint16).reshape(M, F)).astype(np.float64)
         b = b + ulp_bf16(np.abs(h64) + b)
     assert np.all(np.abs(h - h64) <= b)
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("layer,M", [(0, 1), (5, 3)])
+def test_cpp_qkv_group_on_gpu(tool, tmp_path, layer, M):
+    """linear_group through the C++ mirror on the 12B key layout: q, k and (sliding layer 0)
+    v, or q and k only (full layer 5, K = V), each against the oracle's single linear with
+    the bf16-output bound of test_cpp_w4lin_linear_and_dequant_on_gpu."""
+    if not torch.cuda.is_available():
+        pytest.skip("no GPU")
+    n, k = 32, 64
+    path = str(tmp_path / "g12.safetensors")
+    t = g12_like(path, layers=6, n=n, k=k)
+    x = o.synth_x(M, k, 21)
+    x.tofile(tmp_path / "x.bin")
+    rc, outp, err = run(tool, "qkv", path, PREFIX, layer, M, tmp_path / "x.bin", tmp_path / "y")
+    assert rc == 0, err
+    mods = ["q", "k"] if layer == 5 else ["q", "k", "v"]
+    assert json.loads(outp)["linears"] == len(mods)
+    assert not (tmp_path / "y.v.bin").exists() if layer == 5 else True
+    gam = k * 2.0 ** -24 / (1 - k * 2.0 ** -24)
+    for mname in mods:
+        base = f"{PREFIX}.{layer}.self_attn.{mname}_proj"
+        w = o.dequant(t[base + ".weight_packed"].numpy(),
+                      t[base + ".weight_scale"].view(torch.int16).numpy().view(np.uint16))
+        ref32 = o.matmul_f32(x, w)
+        _, mag = o.matmul_f64(x, w)
+        y = o.bf16_to_f32(np.fromfile(tmp_path / f"y.{mname}.bin", dtype=np.uint16).reshape(M, n)).astype(np.float64)
+        ulp = 2.0 ** (np.floor(np.log2(np.maximum(np.abs(ref32), 2.0 ** -126))) - 7)
+        assert np.all(np.abs(y - ref32) <= ulp + 2 * gam * mag), mname
+
+
+@pytest.mark.gpu
+def test_cpp_lm_head_on_gpu(tool, tmp_path):
+    """lm_head through the C++ mirror on the tied embedding of a checkpoint file: logits
+    within the bound of tests/test_gpu_lm_head.py, top-k equal to the oracle's top-k of
+    the same logits."""
+    if not torch.cuda.is_available():
+        pytest.skip("no GPU")
+    V, K, M, k = 3000, 256, 2, 7
+    rng = np.random.Generator(np.random.PCG64(31))
+    e = o.f32_to_bf16(rng.standard_normal((V, K), dtype=np.float32) * np.float32(0.05))
+    name = "model.language_model.embed_tokens.weight"
+    path = str(tmp_path / "head.safetensors")
+    save_file({name: torch.from_numpy(e.view(np.int16).copy()).view(torch.bfloat16)}, path)
+    x = o.synth_x(M, K, 32)
+    x.tofile(tmp_path / "x.bin")
+    rc, outp, err = run(tool, "head", path, name, M, tmp_path / "x.bin", 30.0, k, tmp_path / "h")
+    assert rc == 0, err
+    assert json.loads(outp) == {"V": V, "K": K, "M": M, "topk": k}
+    lg = np.fromfile(tmp_path / "h.logits.bin", dtype=np.float32).reshape(M, V)
+    vals = np.fromfile(tmp_path / "h.values.bin", dtype=np.float32).reshape(M, k)
+    idx = np.fromfile(tmp_path / "h.indices.bin", dtype=np.int32).reshape(M, k)
+    ref, raw, mag = o.lm_head(x, e, 30.0)
+    eps = 2.0 ** -24
+    gam = K * eps / (1 - K * eps)
+    tol = 2 * gam * mag + 4 * eps * (np.abs(raw) + np.abs(ref)) + 2.0 ** -140
+    assert np.all(np.abs(lg.astype(np.float64) - ref) <= tol)
+    ov, oi = o.topk(lg, k)
+    assert np.array_equal(oi, idx) and np.array_equal(ov.view(np.uint32), vals.view(np.uint32))
+
+
+def test_cpp_head_rejects_non_bf16_embedding(tool, tmp_path):
+    """A head tensor that is not bf16 [V, K] fails before any device call."""
+    path = str(tmp_path / "bad.safetensors")
+    save_file({"e": torch.zeros((4, 8), dtype=torch.float32)}, path)
+    (tmp_path / "x.bin").write_bytes(b"\0" * 16)
+    rc, _, err = run(tool, "head", path, "e", 1, tmp_path / "x.bin", 30.0, 1, tmp_path / "h")
+    assert rc != 0 and "not bf16" in err
