@@ -833,8 +833,11 @@ struct SkinnyArgs {
 
 constexpr int SK_P = 4;  // weight prefetch depth (chunks); even, for the two-slot x ring
 
-template <int MT, bool G32>
-__global__ void __launch_bounds__(256) skinny_kernel(SkinnyArgs a) {
+// NW waves of 16 W rows per workgroup (4 or 8): 8 halves the x traffic from L2
+// (x is staged once per 16 * NW rows of W).
+template <int MT, bool G32, int NW = 4>
+__global__ void __launch_bounds__(64 * NW) skinny_kernel(SkinnyArgs a) {
+  constexpr int NTH = 64 * NW;
   constexpr int P = SK_P;
   // x rows of 256 halves as 4 groups of 64 (one lane group c each), every group padded
   // to 72 halves and every row to 304: the A-fragment reads (16 rows, lane groups
@@ -849,7 +852,7 @@ __global__ void __launch_bounds__(256) skinny_kernel(SkinnyArgs a) {
   const int m0 = blockIdx.y * (16 * MT);
   const uint32_t* pkrow;
   const uint16_t* scrow;
-  weight_row(a.pk, a.sc, a.pk2, a.sc2, a.pair_f, (int)blockIdx.x * 64 + 16 * wave + r, a.N, a.K,
+  weight_row(a.pk, a.sc, a.pk2, a.sc2, a.pair_f, (int)blockIdx.x * (16 * NW) + 16 * wave + r, a.N, a.K,
              a.groups_per_row, pkrow, scrow);
 
   // weight ring: chunk k -> slot k % P; lane (r, c) holds the 32-column chunks
@@ -868,12 +871,12 @@ __global__ void __launch_bounds__(256) skinny_kernel(SkinnyArgs a) {
   // x staging: thread t moves vectors t + 256 i (i < 2*MT) of the [16*MT][256] chunk.
   // The register ring is an ext_vector value (not an array) so that it never lives
   // in scratch memory.
-  constexpr int XV = 2 * MT;
+  constexpr int XV = 512 * MT / NTH;
   typedef uint32_t xvec_t __attribute__((ext_vector_type(4 * XV)));
   auto xload = [&](xvec_t& xr, int k) __attribute__((always_inline)) {
 #pragma unroll
     for (int i = 0; i < XV; ++i) {
-      const int v = (int)threadIdx.x + 256 * i;
+      const int v = (int)threadIdx.x + NTH * i;
       const int row = v >> 5, col = (v & 31) * 8;
       const int m = min(m0 + row, a.M - 1);
       const u32x4 t = *reinterpret_cast<const u32x4*>(a.x + (int64_t)m * a.K + k * 256 + col);
@@ -886,7 +889,7 @@ __global__ void __launch_bounds__(256) skinny_kernel(SkinnyArgs a) {
   auto xstore = [&](const xvec_t& xr, int buf) __attribute__((always_inline)) {
 #pragma unroll
     for (int i = 0; i < XV; ++i) {
-      const int v = (int)threadIdx.x + 256 * i;
+      const int v = (int)threadIdx.x + NTH * i;
       const int row = v >> 5, col = (v & 31) * 8;
       *reinterpret_cast<u32x4*>(&xs[buf][row][(col >> 6) * XG + (col & 63)]) =
           u32x4{xr[4 * i], xr[4 * i + 1], xr[4 * i + 2], xr[4 * i + 3]};
@@ -961,7 +964,7 @@ __global__ void __launch_bounds__(256) skinny_kernel(SkinnyArgs a) {
   if (k + 2 < a.nk) iter(k + 2, std::integral_constant<int, 2>{});
 
   // D layout: lane (n = r, c) holds D[m = 4c + i][n]
-  const int nout = (int)blockIdx.x * 64 + 16 * wave + r;
+  const int nout = (int)blockIdx.x * (16 * NW) + 16 * wave + r;
   if (a.pair_f) {
     // Lanes r and r ^ 8 hold gate and up of row f for the same m; per pair of
     // rows m, m + 1 the gate lane finishes m and the up lane m + 1 (all lanes
@@ -1646,16 +1649,30 @@ hipError_t w4l_skinny(const uint16_t* x, const int32_t* pk, const uint16_t* sc, 
     const int v = atoi(e);
     if (v == 1 || v == 2 || v == 4) mt = v;
   }
-  const dim3 grid((unsigned)((N + 63) / 64), (unsigned)((M + 16 * mt - 1) / (16 * mt))), block(256);
+  // Eight waves (128 W rows) per workgroup when that still gives >= 240
+  // workgroups: x is then re-read from L2 half as often (12B gate/up, M = 64:
+  // 36.6 -> 30.7 us; M = 16 / 32: 22.0 / 26.6 -> 19.8 / 23.1).  Smaller N keeps
+  // four waves so the grid still fills the GPU.  W4A16_SKINNY_NW=<4|8> overrides
+  // it for tuning.
+  int nw = ((N + 127) / 128) * ((M + 16 * mt - 1) / (16 * mt)) >= 240 ? 8 : 4;
+  if (const char* e = getenv("W4A16_SKINNY_NW")) nw = atoi(e) == 8 ? 8 : 4;
+  const dim3 grid((unsigned)((N + 16 * nw - 1) / (16 * nw)), (unsigned)((M + 16 * mt - 1) / (16 * mt))),
+      block(64 * nw);
   const bool g32 = group == 32;
-#define W4_SK(MT_)                                                                                   \
-  do {                                                                                               \
-    if (g32) hipLaunchKernelGGL((w4k::skinny_kernel<MT_, true>), grid, block, 0, st, a);            \
-    else hipLaunchKernelGGL((w4k::skinny_kernel<MT_, false>), grid, block, 0, st, a);               \
+#define W4_SK(MT_, NW_)                                                                               \
+  do {                                                                                                \
+    if (g32) hipLaunchKernelGGL((w4k::skinny_kernel<MT_, true, NW_>), grid, block, 0, st, a);        \
+    else hipLaunchKernelGGL((w4k::skinny_kernel<MT_, false, NW_>), grid, block, 0, st, a);           \
   } while (0)
-  if (mt == 1) W4_SK(1);
-  else if (mt == 2) W4_SK(2);
-  else W4_SK(4);
+#define W4_SK_N(MT_)       \
+  do {                     \
+    if (nw == 8) W4_SK(MT_, 8); \
+    else W4_SK(MT_, 4);    \
+  } while (0)
+  if (mt == 1) W4_SK_N(1);
+  else if (mt == 2) W4_SK_N(2);
+  else W4_SK_N(4);
+#undef W4_SK_N
 #undef W4_SK
   return hipGetLastError();
 }

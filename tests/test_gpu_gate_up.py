@@ -142,6 +142,19 @@ def test_gate_up_gelu_vs_oracle(M, F, K, group, x_f32, h_f32, bf16_dots):
     check(h, x, pk_g, sc_g, pk_u, sc_u, K, group, h_f32, bf16_dots)
 
 
+@pytest.mark.parametrize("M", [20, 64])
+def test_gate_up_gelu_12b_skinny_eight_waves(M):
+    """12B gate/up (F = 15360, K = 3840) at M = 20 and 64: the skinny kernel with eight
+    waves (128 W rows) per workgroup, pair mode; the oracle on every 7th row f."""
+    F, K = 15360, 3840
+    say(f"gate_up_gelu 12B skinny M={M}")
+    pk_g, sc_g, pk_u, sc_u = weights(F, K, 4700, 32)
+    x = o.synth_x(M, K, 4701 + M)
+    h = run_gpu(x, pk_g, sc_g, pk_u, sc_u, 32, False, True, False)
+    f = np.arange(0, F, 7)
+    check(h[:, f], x, pk_g[f], sc_g[f], pk_u[f], sc_u[f], K, 32, True, False)
+
+
 @pytest.mark.parametrize("h_f32", [True, False])
 def test_gate_up_gelu_one_pass_without_workspace(h_f32):
     """E2B gate/up at M = 48: with an empty workspace the call takes the one-pass
