@@ -1111,10 +1111,9 @@ __global__ void __launch_bounds__(64 * WS * KS) prefill_kernel(PrefillArgs a) {
   xvec_t xreg0, xreg1;
   xload(xreg0, 0);
   xload(xreg1, min(1, a.ns - 1));
-  wload(std::integral_constant<int, 0>{}, 0);
-  wload(std::integral_constant<int, 1>{}, min(1, a.ns - 1));
-  if constexpr (P > 2) wload(std::integral_constant<int, 2>{}, min(2, a.ns - 1));
-  if constexpr (P > 3) wload(std::integral_constant<int, 3>{}, min(3, a.ns - 1));
+  static_for<0, P>([&](auto i_c) __attribute__((always_inline)) {
+    wload(i_c, min((int)decltype(i_c)::value, a.ns - 1));
+  });
   xstore(xreg0, 0);
   __syncthreads();
 
@@ -1173,16 +1172,13 @@ __global__ void __launch_bounds__(64 * WS * KS) prefill_kernel(PrefillArgs a) {
     else xstore(xreg0, (s + 1) & 1);
     __syncthreads();
   };
+  static_assert(P % 2 == 0, "the unrolled ring alternates the two x register slots");
   int s = 0;
-  for (; s + P <= a.ns; s += P) {
-    iter(s, std::integral_constant<int, 0>{});
-    iter(s + 1, std::integral_constant<int, 1>{});
-    if constexpr (P > 2) iter(s + 2, std::integral_constant<int, 2>{});
-    if constexpr (P > 3) iter(s + 3, std::integral_constant<int, 3>{});
-  }
-  if (s < a.ns) iter(s, std::integral_constant<int, 0>{});
-  if constexpr (P > 1) if (s + 1 < a.ns) iter(s + 1, std::integral_constant<int, 1>{});
-  if constexpr (P > 2) if (s + 2 < a.ns) iter(s + 2, std::integral_constant<int, 2>{});
+  for (; s + P <= a.ns; s += P)
+    static_for<0, P>([&](auto i_c) __attribute__((always_inline)) { iter(s + decltype(i_c)::value, i_c); });
+  static_for<0, P - 1>([&](auto i_c) __attribute__((always_inline)) {
+    if (s + decltype(i_c)::value < a.ns) iter(s + decltype(i_c)::value, i_c);
+  });
   // the last MFMAs must finish before their AGPRs are read (16-pass MFMA: >= 18 wait states)
   asm volatile("s_nop 7\n\ts_nop 7\n\ts_nop 7\n\ts_nop 7" ::: "memory");
 
@@ -1284,6 +1280,39 @@ __global__ void __launch_bounds__(256) splitk_finalize_kernel(const float* __res
   const int64_t total = (int64_t)M * cols;
   const int64_t plane = (int64_t)M * N;
   const int64_t stride = (int64_t)gridDim.x * blockDim.x;
+  if ((cols & 3) == 0 && (N & 3) == 0) {
+    // four consecutive outputs per thread (16-byte loads; in pair mode four
+    // consecutive f map to four consecutive virtual rows of the same tile)
+    for (int64_t i4 = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i4 < total / 4; i4 += stride) {
+      const int64_t i = 4 * i4;
+      const int m = (int)(i / cols), col = (int)(i % cols);
+      const int vc = pair_f ? (((col >> 3) << 4) | (col & 7)) : col;
+      const float4* pv = reinterpret_cast<const float4*>(part + (int64_t)m * N + vc);
+      float4 g = pv[0], u = make_float4(0.f, 0.f, 0.f, 0.f);
+      if (pair_f) u = pv[2];  // + 8 floats
+      for (int q = 1; q < kq; ++q) {
+        const float4 t = pv[q * (plane / 4)];
+        g.x += t.x; g.y += t.y; g.z += t.z; g.w += t.w;
+        if (pair_f) {
+          const float4 w = pv[q * (plane / 4) + 2];
+          u.x += w.x; u.y += w.y; u.z += w.z; u.w += w.w;
+        }
+      }
+      if (pair_f) {
+        store_gelu_mul(y, y_f32, bf16_dots, i, g.x, u.x);
+        store_gelu_mul(y, y_f32, bf16_dots, i + 1, g.y, u.y);
+        store_gelu_mul(y, y_f32, bf16_dots, i + 2, g.z, u.z);
+        store_gelu_mul(y, y_f32, bf16_dots, i + 3, g.w, u.w);
+      } else if (y_f32) {
+        reinterpret_cast<float4*>(y)[i4] = g;
+      } else {
+        const uint32_t lo = f32_to_bf16_rne(g.x) | (f32_to_bf16_rne(g.y) << 16);
+        const uint32_t hi = f32_to_bf16_rne(g.z) | (f32_to_bf16_rne(g.w) << 16);
+        reinterpret_cast<uint2*>(y)[i4] = make_uint2(lo, hi);
+      }
+    }
+    return;
+  }
   for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < total; i += stride) {
     const int m = (int)(i / cols), col = (int)(i % cols);
     if (pair_f) {
@@ -1838,7 +1867,8 @@ hipError_t w4l_splitk(const uint16_t* x, const int32_t* pk, const uint16_t* sc, 
 #undef W4_SKQ
   hipError_t e = hipGetLastError();
   if (e != hipSuccess) return e;
-  const int64_t outs = M * (pair ? pair->F : N);
+  const int64_t cols = pair ? pair->F : N;
+  const int64_t outs = (cols % 4 == 0 && Nv % 4 == 0) ? M * cols / 4 : M * cols;  // threads (4 outputs each when aligned)
   const int block_f = 256;
   hipLaunchKernelGGL(w4k::splitk_finalize_kernel, dim3(grid_for(outs, block_f)), dim3(block_f), 0, st, part, kq,
                      (int)M, (int)Nv, y, y_f32, pair ? (int)pair->F : 0, pair ? pair->bf16_dots : 0);
