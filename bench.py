@@ -419,7 +419,12 @@ def main() -> int:
         cfgs += [(f"E2B_{n}", 1, K, N) for n, K, N in [("q", 1536, 2048), ("kv", 1536, 256), ("o", 2048, 1536),
                                                         ("gate_up", 1536, 12288), ("down", 6144, 1536)]]
         cfgs += [(f"12B_{n}", 1, K, N) for n, K, N in LAYER_12B]
+        # full-attention layers of the 12B (no v_proj): q 3840->8192, k 3840->512, o 8192->3840
+        cfgs += [("12B_full_q", 1, 3840, 8192), ("12B_full_k", 1, 3840, 512), ("12B_full_o", 1, 8192, 3840)]
         cfgs += [(f"C4_M{M}", M, 3840, 30720) for M in (8, 16, 32, 64)]
+        # configs[3] covers every config-2 weight at M = 8..64: the other linears of the layer
+        cfgs += [(f"C4_{n}_M{M}", M, K, N) for M in (8, 16, 32, 64)
+                 for n, K, N in LAYER_12B if n not in ("gate_up", "v")]
         cfgs += [("C5_gate_up", 2048, 3840, 30720), ("C5_down", 2048, 15360, 3840)]
         for name, M, K, N in cfgs:
             r = time_config(torch, w4a16, o, M, K, N)

@@ -211,7 +211,9 @@ int w4a16_linear_group(const void* x, int32_t x_dtype, int32_t n, const int32_t*
   } else if (workspace != nullptr && !aligned16(workspace)) {
     return fail(W4A16_EINVAL_PTR, "%s: workspace is not 16-byte aligned", fn);
   }
-  if (w4l_group_fused(M, K, nterms))
+  int64_t ntot = 0;
+  for (int j = 0; j < n; ++j) ntot += 16 * ((N[j] + 15) / 16);
+  if (w4l_group_fused(M, ntot, K, nterms))
     return hip_status(w4l_gemv_group(planes, nterms, n, pk, sc, y, N, y_f32, M, K, group, st), fn);
   for (int j = 0; j < n; ++j)
     if (N[j] && (rc = hip_status(w4l_linear(planes, nterms, pk[j], sc[j], y[j], y_f32, M, N[j], K, group, st), fn)))

@@ -548,7 +548,9 @@ __global__ void __launch_bounds__(1024) gemv_kernel(GemvArgs a) {
 // counter: a conditional load makes every later wait fall back to "all loads
 // done".)  Tiles past N (odd tile counts) recompute the last tile and are not
 // written.
-template <int NT, int NST, int XPT, int TPW, bool G32>
+// MR: rows of x the epilogue covers, 4 (M <= 4) or 16 (M <= 16; the MFMA's A
+// operand holds 16 rows of x either way, rows past M repeat row M-1).
+template <int NT, int NST, int XPT, int TPW, bool G32, int MR = 4>
 __global__ void __launch_bounds__(1024) gemv_fast_kernel(GemvArgs a) {
   extern __shared__ __attribute__((aligned(16))) uint16_t lds[];
   const int lane = threadIdx.x & 63;
@@ -632,16 +634,17 @@ __global__ void __launch_bounds__(1024) gemv_fast_kernel(GemvArgs a) {
   }
   mfma_drain<TPW>(acc);
 
-  float* red = reinterpret_cast<float*>(lds + NT * plane);  // [TPW][waves][4][16]
-  if (c == 0) {
+  // D: lane (r, c) holds rows m = 4c + i of column r; MR = 4 keeps c == 0 only
+  float* red = reinterpret_cast<float*>(lds + NT * plane);  // [TPW][waves][MR][16]
+  if (MR == 16 || c == 0) {
 #pragma unroll
     for (int tp = 0; tp < TPW; ++tp)
 #pragma unroll
-      for (int i = 0; i < 4; ++i) red[((tp * nwaves + wave) * 4 + i) * 16 + r] = acc[tp][i];
+      for (int i = 0; i < 4; ++i) red[((tp * nwaves + wave) * MR + (MR == 16 ? 4 * c : 0) + i) * 16 + r] = acc[tp][i];
   }
   __syncthreads();
-  if ((int)threadIdx.x < 16 * 4 * TPW) {
-    const int tp = threadIdx.x >> 6, m = (threadIdx.x >> 4) & 3, rr = threadIdx.x & 15;
+  for (int t = (int)threadIdx.x; t < 16 * MR * TPW; t += (int)blockDim.x) {
+    const int tp = t / (16 * MR), m = (t >> 4) % MR, rr = t & 15;
     const int n = (bt + tp) * 16 + rr;
     if (a.pair_f) {
       // gate row rr < 8 of the tile and its up row rr + 8
@@ -649,14 +652,14 @@ __global__ void __launch_bounds__(1024) gemv_fast_kernel(GemvArgs a) {
       if (rr < 8 && m < a.M && f < a.pair_f) {
         float g = 0.f, u = 0.f;
         for (int w = 0; w < nwaves; ++w) {
-          g += red[((tp * nwaves + w) * 4 + m) * 16 + rr];
-          u += red[((tp * nwaves + w) * 4 + m) * 16 + rr + 8];
+          g += red[((tp * nwaves + w) * MR + m) * 16 + rr];
+          u += red[((tp * nwaves + w) * MR + m) * 16 + rr + 8];
         }
         store_gelu_mul(a.y, a.y_f32, a.bf16_dots, (int64_t)m * a.pair_f + f, g, u);
       }
     } else if (m < a.M && n < N) {
       float v = 0.f;
-      for (int w = 0; w < nwaves; ++w) v += red[((tp * nwaves + w) * 4 + m) * 16 + rr];
+      for (int w = 0; w < nwaves; ++w) v += red[((tp * nwaves + w) * MR + m) * 16 + rr];
       if (a.y_f32) reinterpret_cast<float*>(gs.y)[(int64_t)m * N + n] = v;
       else reinterpret_cast<uint16_t*>(gs.y)[(int64_t)m * N + n] = (uint16_t)f32_to_bf16_rne(v);
     }
@@ -1398,6 +1401,20 @@ hipError_t w4l_fill_zero(void* p, int64_t bytes, hipStream_t st) {
 }
 
 
+bool w4l_gemv16_plan(int64_t M, int64_t N, int64_t K, int nterms, int* nst_out, int* waves_out, int* xpt_out);
+// 4 < M <= 16 through the GEMV when its plan holds and every 16-row tile
+// re-reading x from L2 stays under 40 MiB (W4A16_GEMV16_XBYTES overrides):
+// measured on the 12B and E2B rows, the GEMV wins 1.2-1.9x below that (q, k/v, o,
+// E2B) and the skinny kernel, whose workgroups share x over 64-128 rows, wins
+// above it (12B gate/up, full-layer q at M = 16).
+bool w4l_gemv16_ok(int64_t M, int64_t N, int64_t K, int nterms) {
+  int nst, waves, xpt;
+  if (!w4l_gemv16_plan(M, N, K, nterms, &nst, &waves, &xpt)) return false;
+  int64_t max_bytes = 40ll << 20;
+  if (const char* e = getenv("W4A16_GEMV16_XBYTES")) max_bytes = atoll(e);
+  return (N + 15) / 16 * M * K * 2 <= max_bytes;
+}
+
 bool w4l_gemv_ok(int64_t M, int64_t K, int nterms) {
   return M >= 1 && M <= 4 && (int64_t)nterms * M * K * 2 + 16 * 4 * 16 * 4 <= 65536;
 }
@@ -1447,6 +1464,33 @@ bool w4l_gemv_fast_plan(int64_t M, int64_t N, int64_t K, int nterms, int* nst_ou
   return true;
 }
 
+// Straight-line GEMV for 4 < M <= 16 (bf16 x): the same kernel with a 16-row
+// epilogue.  As many waves as K / 256 allows (<= 16) so that each thread stages
+// at most 8 x vectors; x [M][K] sits in LDS whole (up to 160 KB on gfx950).
+// W4A16_GEMV16=0 turns the route off (tuning).
+bool w4l_gemv16_plan(int64_t M, int64_t N, int64_t K, int nterms, int* nst_out, int* waves_out, int* xpt_out) {
+  if (nterms != 1 || M <= 4 || M > 16 || K % w4k::GSTEP != 0 || N <= 0) return false;
+  if (const char* e = getenv("W4A16_GEMV16"))
+    if (atoi(e) == 0) return false;
+  const int64_t steps = K / w4k::GSTEP;
+  int nst = 0;
+  for (int p = 1; p <= 6 && !nst; ++p)
+    if (steps % p == 0 && steps / p <= 16) nst = p;
+  if (!nst) return false;
+  const int waves = (int)(steps / nst);
+  const int64_t nvec = M * K / 8;
+  const int64_t per = (nvec + 64 * waves - 1) / (64 * waves);
+  int xpt = 1;
+  while (xpt < per) xpt *= 2;
+  if (xpt > 8) return false;
+  const int64_t lds = M * K * 2 + (int64_t)waves * 16 * 16 * 4;
+  if (lds > 160 * 1024) return false;
+  *nst_out = nst;
+  *waves_out = waves;
+  *xpt_out = xpt;
+  return true;
+}
+
 // Streaming GEMV plan (opt-in with W4A16_GEMV_STREAM): waves per tile W,
 // chunk steps NST, chunks per wave CPW with W * CPW * NST == K / GSTEP.  Few
 // tiles -> more waves per tile.  W4A16_GEMV_W / W4A16_GEMV_NST override.
@@ -1486,6 +1530,52 @@ bool w4l_gemv_stream_plan(int64_t M, int64_t N, int64_t K, int nterms, int* w_ou
 // Launch of gemv_fast_kernel for a filled GemvArgs: the template arguments
 // follow the plan (x planes, steps per wave, x vectors per thread, tiles per
 // workgroup, group 32).
+// LDS above 64 KB per workgroup needs the kernel's attribute raised once.
+template <class Kern>
+static hipError_t allow_big_lds(Kern k, size_t lds) {
+  if (lds <= 64 * 1024) return hipSuccess;
+  return hipFuncSetAttribute(reinterpret_cast<const void*>(k), hipFuncAttributeMaxDynamicSharedMemorySize,
+                             160 * 1024);
+}
+
+// M <= 16 form (mr = 16, bf16 x, one tile per workgroup): nst 1..2, xpt 1..8.
+static hipError_t gemv16_launch(const w4k::GemvArgs& a, int nst, int waves, int xpt, int nblocks, bool g32,
+                                hipStream_t st) {
+  const size_t lds = (size_t)a.M * a.K * 2 + (size_t)waves * 16 * 16 * 4;
+  const dim3 grid((unsigned)nblocks), block(64 * waves);
+  hipError_t e = hipSuccess;
+#define W4_G16(NST_, XPT_)                                                                  \
+  do {                                                                                      \
+    if (g32) {                                                                              \
+      auto k = w4k::gemv_fast_kernel<1, NST_, XPT_, 1, true, 16>;                           \
+      if ((e = allow_big_lds(k, lds)) != hipSuccess) return e;                              \
+      hipLaunchKernelGGL(k, grid, block, lds, st, a);                                       \
+    } else {                                                                                \
+      auto k = w4k::gemv_fast_kernel<1, NST_, XPT_, 1, false, 16>;                          \
+      if ((e = allow_big_lds(k, lds)) != hipSuccess) return e;                              \
+      hipLaunchKernelGGL(k, grid, block, lds, st, a);                                       \
+    }                                                                                       \
+  } while (0)
+#define W4_G16_X(NST_)                      \
+  switch (xpt) {                            \
+    case 1: W4_G16(NST_, 1); break;         \
+    case 2: W4_G16(NST_, 2); break;         \
+    case 4: W4_G16(NST_, 4); break;         \
+    default: W4_G16(NST_, 8); break;        \
+  }
+  switch (nst) {
+    case 1: W4_G16_X(1); break;
+    case 2: W4_G16_X(2); break;
+    case 3: W4_G16_X(3); break;
+    case 4: W4_G16_X(4); break;
+    case 5: W4_G16_X(5); break;
+    default: W4_G16_X(6); break;
+  }
+#undef W4_G16_X
+#undef W4_G16
+  return hipGetLastError();
+}
+
 static hipError_t gemv_fast_launch(const w4k::GemvArgs& a, int nterms, int nst, int waves, int xpt, int tpw,
                                    int nblocks, bool g32, hipStream_t st) {
   const size_t lds = (size_t)nterms * a.M * a.K * 2 + (size_t)tpw * waves * 4 * 16 * 4;
@@ -1528,6 +1618,29 @@ hipError_t w4l_gemv(const uint16_t* x_planes, int nterms, const int32_t* pk, con
                     void* y, int y_f32, int64_t M, int64_t N, int64_t K, int32_t group,
                     hipStream_t st, const W4Pair* pair) {
   if (pair) N = 16 * ((pair->F + 7) / 8);
+  if (M > 4) {
+    int nst, waves, xpt;
+    if (!w4l_gemv16_plan(M, N, K, nterms, &nst, &waves, &xpt)) return hipErrorInvalidValue;
+    w4k::GemvArgs a{};
+    a.x = x_planes;
+    a.pk = reinterpret_cast<const uint32_t*>(pk);
+    a.sc = sc;
+    a.y = y;
+    a.M = (int)M;
+    a.N = (int)N;
+    a.K = (int)K;
+    a.group_chunks = group / 32;
+    a.groups_per_row = (int)(K / group);
+    a.y_f32 = y_f32;
+    a.steps = (int)(K / w4k::GSTEP);
+    if (pair) {
+      a.pk2 = reinterpret_cast<const uint32_t*>(pair->pk_up);
+      a.sc2 = pair->sc_up;
+      a.pair_f = (int)pair->F;
+      a.bf16_dots = pair->bf16_dots;
+    }
+    return gemv16_launch(a, nst, waves, xpt, (int)((N + 15) / 16), group == 32, st);
+  }
   if (!pair && getenv("W4A16_GEMV_STREAM")) {
     int w, nst, cpw, xpt;
     if (w4l_gemv_stream_plan(M, N, K, nterms, &w, &nst, &cpw, &xpt)) {
@@ -1879,6 +1992,7 @@ hipError_t w4l_linear(const uint16_t* x_planes, int nterms, const int32_t* pk, c
                       void* y, int y_f32, int64_t M, int64_t N, int64_t K, int32_t group,
                       hipStream_t st) {
   if (w4l_gemv_ok(M, K, nterms)) return w4l_gemv(x_planes, nterms, pk, sc, y, y_f32, M, N, K, group, st);
+  if (w4l_gemv16_ok(M, N, K, nterms)) return w4l_gemv(x_planes, nterms, pk, sc, y, y_f32, M, N, K, group, st);
   if (w4l_prefill_ok(M, K, nterms)) return w4l_prefill(x_planes, pk, sc, y, y_f32, M, N, K, group, st);
   // W4A16_PF_SMALL=1: tuning switch, 4 < M <= 64 through the 32x32 kernel
   if (getenv("W4A16_PF_SMALL") && nterms == 1 && M > 4 && K % 64 == 0)
@@ -1931,6 +2045,7 @@ PairRoute pair_route(int64_t M, int64_t F, int64_t K, int nterms) {
   int nst, waves, xpt, tpw;
   if (w4l_gemv_ok(M, K, nterms) && w4l_gemv_fast_plan(M, 16 * ((F + 7) / 8), K, nterms, &nst, &waves, &xpt, &tpw))
     return PAIR_GEMV;
+  if (w4l_gemv16_ok(M, 16 * ((F + 7) / 8), K, nterms)) return PAIR_GEMV;
   if (w4l_prefill_ok(M, K, nterms)) return PAIR_PREFILL;
   if (getenv("W4A16_PF_SMALL") && nterms == 1 && M > 4 && K % 64 == 0) return PAIR_PREFILL;
   if (nterms == 1 && K % 256 == 0) return PAIR_SKINNY;
@@ -1961,8 +2076,9 @@ hipError_t w4l_gelu_mul(const float* g, const float* u, void* h, int h_f32, int 
   return hipGetLastError();
 }
 
-bool w4l_group_fused(int64_t M, int64_t K, int nterms) {
+bool w4l_group_fused(int64_t M, int64_t Ntot, int64_t K, int nterms) {
   int nst, waves, xpt, tpw;
+  if (M > 4) return w4l_gemv16_ok(M, Ntot, K, nterms);
   return w4l_gemv_ok(M, K, nterms) && w4l_gemv_fast_plan(M, 16, K, nterms, &nst, &waves, &xpt, &tpw);
 }
 
@@ -1970,7 +2086,10 @@ hipError_t w4l_gemv_group(const uint16_t* x_planes, int nterms, int n, const int
                           const uint16_t* const* sc, void* const* y, const int64_t* N, int y_f32, int64_t M, int64_t K,
                           int32_t group, hipStream_t st) {
   int nst, waves, xpt, tpw;
-  if (n < 1 || n > 4 || !w4l_gemv_ok(M, K, nterms) || !w4l_gemv_fast_plan(M, 16, K, nterms, &nst, &waves, &xpt, &tpw))
+  const bool m16 = M > 4;
+  if (n < 1 || n > 4) return hipErrorInvalidValue;
+  if (m16 ? !w4l_gemv16_plan(M, 16, K, nterms, &nst, &waves, &xpt)
+          : (!w4l_gemv_ok(M, K, nterms) || !w4l_gemv_fast_plan(M, 16, K, nterms, &nst, &waves, &xpt, &tpw)))
     return hipErrorInvalidValue;
   w4k::GemvArgs a{};
   a.x = x_planes;
@@ -1996,5 +2115,6 @@ hipError_t w4l_gemv_group(const uint16_t* x_planes, int nterms, int n, const int
   a.y = a.gy[0];
   a.N = a.gN[0];
   if (tiles == 0) return hipSuccess;
+  if (m16) return gemv16_launch(a, nst, waves, xpt, (int)tiles, group == 32, st);
   return gemv_fast_launch(a, nterms, nst, waves, xpt, 1, (int)tiles, group == 32, st);
 }

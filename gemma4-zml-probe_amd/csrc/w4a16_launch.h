@@ -31,6 +31,8 @@ struct W4Pair {
 
 // Decode GEMV path (M <= 4, x planes fit in 64 KiB of LDS).
 bool w4l_gemv_ok(int64_t M, int64_t K, int nterms);
+// 4 < M <= 16 through the same GEMV kernel (bf16 x, small N); w4l_gemv takes it.
+bool w4l_gemv16_ok(int64_t M, int64_t N, int64_t K, int nterms);
 int w4l_gemv_waves(int64_t N, int64_t K);
 bool w4l_gemv_stream_plan(int64_t M, int64_t N, int64_t K, int nterms, int* w, int* nst, int* cpw, int* xpt);
 bool w4l_gemv_fast_plan(int64_t M, int64_t N, int64_t K, int nterms, int* nst, int* waves, int* xpt, int* tpw);
@@ -55,7 +57,7 @@ hipError_t w4l_prefill(const uint16_t* x, const int32_t* pk, const uint16_t* sc,
 // Weight group: n <= 4 linears [N_j, K] that read the same x (q, k, v), one
 // launch of the straight-line GEMV when w4l_group_fused; otherwise the caller
 // runs w4l_linear per weight.
-bool w4l_group_fused(int64_t M, int64_t K, int nterms);
+bool w4l_group_fused(int64_t M, int64_t Ntot, int64_t K, int nterms);
 hipError_t w4l_gemv_group(const uint16_t* x_planes, int nterms, int n, const int32_t* const* pk,
                           const uint16_t* const* sc, void* const* y, const int64_t* N, int y_f32, int64_t M, int64_t K,
                           int32_t group, hipStream_t st);

@@ -109,6 +109,20 @@ void W4Lin::linear(const uint16_t* x, float* y, int64_t m, hipStream_t stream) c
         "W4Lin.linear");
 }
 
+size_t W4Lin::workspace(int64_t m) const { return w4a16_workspace_size(m, n, k, W4A16_DTYPE_BF16); }
+
+void W4Lin::linear(const uint16_t* x, uint16_t* y, int64_t m, void* workspace, size_t ws_bytes,
+                   hipStream_t stream) const {
+  check(w4a16_linear(x, W4A16_DTYPE_BF16, pk, sc, y, W4A16_DTYPE_BF16, m, n, k, group, 0, workspace, ws_bytes, stream),
+        "W4Lin.linear");
+}
+
+void W4Lin::linear(const uint16_t* x, float* y, int64_t m, void* workspace, size_t ws_bytes,
+                   hipStream_t stream) const {
+  check(w4a16_linear(x, W4A16_DTYPE_BF16, pk, sc, y, W4A16_DTYPE_F32, m, n, k, group, 0, workspace, ws_bytes, stream),
+        "W4Lin.linear");
+}
+
 size_t W4Lin::workspace_f32(int64_t m) const { return w4a16_workspace_size(m, n, k, W4A16_DTYPE_F32); }
 
 void W4Lin::linear_f32(const float* x, float* y, int64_t m, void* workspace, size_t ws_bytes,

@@ -75,6 +75,12 @@ struct W4Lin {
   // y[m, n] = x[m, k] . toW()^T, fp32 accumulate; bf16 x, bf16 or f32 y.
   void linear(const uint16_t* x, uint16_t* y, int64_t m, hipStream_t stream) const;
   void linear(const uint16_t* x, float* y, int64_t m, hipStream_t stream) const;
+  // The same with optional workspace: given workspace(m) bytes, batched shapes whose
+  // one-pass grid cannot fill the GPU (4 < m <= 64 on the smaller rows) split K
+  // across workgroups; 0 bytes or nullptr takes the one-pass route.
+  size_t workspace(int64_t m) const;
+  void linear(const uint16_t* x, uint16_t* y, int64_t m, void* workspace, size_t ws_bytes, hipStream_t stream) const;
+  void linear(const uint16_t* x, float* y, int64_t m, void* workspace, size_t ws_bytes, hipStream_t stream) const;
   // f32 activations (dotPrec with fam = null, engine.zig:530-533): caller workspace of
   // workspace_f32(m) bytes.
   size_t workspace_f32(int64_t m) const;

@@ -123,20 +123,24 @@ int cmd_linear(int argc, char** argv) {
   const w4::W4Lin lin = w4::W4Lin::init(store, argv[3]);
   const auto x = read_file(argv[5], (size_t)(M * lin.k * 2));
   const size_t ybytes = (size_t)(M * lin.n * (f32 ? 4 : 2));
-  void *dx = nullptr, *dy = nullptr;
+  const size_t ws = lin.workspace(M);  // optional: the split-K route on batched shapes
+  void *dx = nullptr, *dy = nullptr, *dws = nullptr;
   hip_ok(hipMalloc(&dx, std::max<size_t>(x.size(), 16)), "hipMalloc x");
   hip_ok(hipMalloc(&dy, std::max<size_t>(ybytes, 16)), "hipMalloc y");
+  if (ws) hip_ok(hipMalloc(&dws, ws), "hipMalloc workspace");
   hip_ok(hipMemcpy(dx, x.data(), x.size(), hipMemcpyHostToDevice), "copy x");
-  if (f32) lin.linear(static_cast<const uint16_t*>(dx), static_cast<float*>(dy), M, nullptr);
-  else lin.linear(static_cast<const uint16_t*>(dx), static_cast<uint16_t*>(dy), M, nullptr);
+  if (f32) lin.linear(static_cast<const uint16_t*>(dx), static_cast<float*>(dy), M, dws, ws, nullptr);
+  else lin.linear(static_cast<const uint16_t*>(dx), static_cast<uint16_t*>(dy), M, dws, ws, nullptr);
   std::vector<char> y(ybytes);
   hip_ok(hipMemcpy(y.data(), dy, ybytes, hipMemcpyDeviceToHost), "copy y");
   write_file(argv[6], y.data(), ybytes);
   (void)hipFree(dx);
   (void)hipFree(dy);
-  std::printf("{\"name\": \"%s\", \"M\": %lld, \"n\": %lld, \"k\": %lld, \"group\": %d, \"y\": \"%s\"}\n",
+  if (dws) (void)hipFree(dws);
+  std::printf("{\"name\": \"%s\", \"M\": %lld, \"n\": %lld, \"k\": %lld, \"group\": %d, \"y\": \"%s\", "
+              "\"workspace\": %zu}\n",
               json_escape(argv[3]).c_str(), (long long)M, (long long)lin.n, (long long)lin.k, lin.group,
-              f32 ? "f32" : "bf16");
+              f32 ? "f32" : "bf16", ws);
   return 0;
 }
 

@@ -116,7 +116,9 @@ CASES = [
     (1, 72, 1024, 32, True, True, False),       # GEMV on f32 x (three bf16 planes)
     (1, 15360, 3840, 32, False, True, False),   # 12B gate/up decode
     (4, 70, 3840, 32, False, True, False),      # M = 4 at K = 3840 -> skinny
-    (5, 33, 256, 32, False, False, False),      # skinny
+    (5, 33, 256, 32, False, False, False),      # 16-row GEMV pair mode
+    (8, 6144, 1536, 32, False, True, False),    # 16-row GEMV pair mode: E2B gate/up at M = 8
+    (16, 72, 1024, 64, False, False, True),     # 16-row GEMV pair mode, group 64, bf16 dots, h bf16
     (17, 9, 512, 32, False, True, False),       # split-K, one real row in the second x block
     (40, 129, 1280, 32, False, True, True),     # split-K, bf16 dots
     (64, 200, 768, 128, False, True, False),    # split-K (400 virtual rows), group 128

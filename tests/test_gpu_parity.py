@@ -230,6 +230,8 @@ C123 = {  # (K, N)
     "E2B_gateup": (1536, 12288), "E2B_down": (6144, 1536),
     "12B_gateup": (3840, 30720), "12B_down": (15360, 3840), "12B_q": (3840, 4096),
     "12B_kv": (3840, 2048), "12B_o": (4096, 3840),
+    # 12B full-attention layers (g12.zig:139-166: no v_proj; q 3840->8192, k 3840->512, o 8192->3840)
+    "12B_full_q": (3840, 8192), "12B_full_k": (3840, 512), "12B_full_o": (8192, 3840),
 }
 
 
@@ -280,6 +282,22 @@ def test_linear_c4_12b_gateup(M):
     ref32 = o.matmul_f32(x, w)
     check_f32(y[:, rows], x, w, K, ref32)
     check_head_argmax(y[:, rows], ref32, len(rows))
+
+
+@pytest.mark.parametrize("M,K,N", [
+    (5, 3840, 4096), (8, 4096, 3840), (13, 1536, 2048), (16, 3840, 2048), (16, 2048, 1536), (12, 256, 40),
+])
+def test_linear_gemv16_route(M, K, N):
+    """4 < M <= 16 on the smaller rows: the straight-line GEMV with its 16-row epilogue
+    (x whole in LDS, up to 160 KB) against the oracle, f32 and bf16 outputs."""
+    say(f"gemv16 M={M} K={K} N={N}")
+    _, pk, sc = o.synth_weights(N, K, 1300 + N)
+    x = o.synth_x(M, K, 1400 + M)
+    w = o.dequant(pk, sc)
+    ref32 = o.matmul_f32(x, w)
+    check_f32(gpu_linear(x, pk, sc, "f32"), x, w, K, ref32)
+    _, mag = o.matmul_f64(x, w)
+    check_bf16(gpu_linear(x, pk, sc, "bf16"), ref32, mag, K)
 
 
 @pytest.mark.parametrize("M,K,N,step", [
@@ -522,7 +540,9 @@ def test_prefill_kernel_small_m(M, N, K, monkeypatch):
     (1, (4096, 2048, 2048), 3840, False, "bf16"),   # 12B q, k, v at decode: one launch
     (3, (17, 0, 33, 5), 512, False, "f32"),        # ragged N, an empty member
     (2, (64, 48), 1536, True, "f32"),               # f32 x
-    (20, (40, 24, 16), 256, False, "bf16"),         # above decode: one launch per weight
+    (20, (40, 24, 16), 256, False, "bf16"),         # above M = 16: one launch per weight
+    (8, (4096, 2048, 2048), 3840, False, "f32"),     # batched decode M = 8: one launch (16-row GEMV)
+    (13, (17, 0, 33, 5), 512, False, "f32"),        # M = 13, ragged N, an empty member
 ])
 def test_linear_group_equals_single_linears(M, Ns, K, x_f32, out):
     """w4a16_linear_group (q, k, v read the same x, engine.zig:552,571,583): every output

@@ -161,7 +161,7 @@ def test_empty_header_and_offsets_checked(tool, tmp_path):
 
 
 @pytest.mark.gpu
-@pytest.mark.parametrize("M,out", [(1, "bf16"), (5, "f32"), (70, "bf16")])
+@pytest.mark.parametrize("M,out", [(1, "bf16"), (5, "f32"), (70, "bf16"), (24, "f32")])
 def test_cpp_w4lin_linear_and_dequant_on_gpu(tool, tmp_path, M, out):
     """W4Lin::init -> linear / toW through the C++ mirror vs the oracle (tolerances of
     test_gpu_parity.py: bit-exact dequant; fp32-accumulate bound for the linear)."""
@@ -179,8 +179,9 @@ def test_cpp_w4lin_linear_and_dequant_on_gpu(tool, tmp_path, M, out):
     assert np.array_equal(np.fromfile(tmp_path / "w.bin", dtype=np.uint16).reshape(n, k), w)
     x = o.synth_x(M, k, 5)
     x.tofile(tmp_path / "x.bin")
-    rc, _, err = run(tool, "linear", path, "blk", M, tmp_path / "x.bin", tmp_path / "y.bin", out)
+    rc, outp, err = run(tool, "linear", path, "blk", M, tmp_path / "x.bin", tmp_path / "y.bin", out)
     assert rc == 0, err
+    assert (json.loads(outp)["workspace"] > 0) == (M == 24)  # M = 24 at N = 96: the split-K route
     ref32 = o.matmul_f32(x, w)
     y64, mag = o.matmul_f64(x, w)
     gam = k * 2.0 ** -24 / (1 - k * 2.0 ** -24)
