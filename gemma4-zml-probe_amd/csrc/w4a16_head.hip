@@ -41,8 +41,9 @@ struct HeadArgs {
 
 // NT: bf16 planes of x (1, or 3 for f32 x).  NST: 32-column steps per wave.
 // XPT: x vectors (16 B) per thread.  Waves = blockDim.x / 64; wave w covers
-// steps [w * NST, (w + 1) * NST), and waves * NST * 32 == K.
-template <int NT, int NST, int XPT>
+// steps [w * NST, (w + 1) * NST), and waves * NST * 32 == K.  MR: rows of x
+// the epilogue covers, 4 or 16 (the MFMA's A operand holds 16 rows either way).
+template <int NT, int NST, int XPT, int MR = 4>
 __global__ void __launch_bounds__(1024) head_logits_kernel(HeadArgs a) {
   extern __shared__ __attribute__((aligned(16))) uint16_t lds[];
   const int lane = threadIdx.x & 63;
@@ -86,19 +87,19 @@ __global__ void __launch_bounds__(1024) head_logits_kernel(HeadArgs a) {
   }
   mfma_drain<1>(acc);
 
-  // D: lane (n = r, c) holds D[m = 4c + i][n]
-  float* red = reinterpret_cast<float*>(lds + NT * plane);  // [waves][4][16]
-  if (c == 0) {
+  // D: lane (n = r, c) holds D[m = 4c + i][n]; MR = 4 keeps c == 0 only
+  float* red = reinterpret_cast<float*>(lds + NT * plane);  // [waves][MR][16]
+  if (MR == 16 || c == 0) {
 #pragma unroll
-    for (int i = 0; i < 4; ++i) red[(wave * 4 + i) * 16 + r] = acc[0][i];
+    for (int i = 0; i < 4; ++i) red[(wave * MR + (MR == 16 ? 4 * c : 0) + i) * 16 + r] = acc[0][i];
   }
   __syncthreads();
-  if ((int)threadIdx.x < 64) {
-    const int m = threadIdx.x >> 4, rr = threadIdx.x & 15;
+  for (int t = (int)threadIdx.x; t < 16 * MR; t += (int)blockDim.x) {
+    const int m = t >> 4, rr = t & 15;
     const int nout = (int)blockIdx.x * 16 + rr;
     if (m < a.M && nout < a.V) {
       float v = 0.f;
-      for (int w = 0; w < nwaves; ++w) v += red[(w * 4 + m) * 16 + rr];
+      for (int w = 0; w < nwaves; ++w) v += red[(w * MR + m) * 16 + rr];
       // softcap as the reference orders it: scale by 1/cap, tanh, scale by cap
       if (a.cap > 0.f) v = tanhf(v * (1.0f / a.cap)) * a.cap;
       // NaN (a NaN weight or activation) as the canonical quiet NaN: the sign of a
@@ -223,21 +224,44 @@ static bool head_plan(int64_t K, int* nst, int* waves) {
   return true;
 }
 
+// More rows per launch (5..16) use the MR = 16 epilogue and the plan with the
+// most waves (<= 16), so that each thread stages <= 8 x vectors; x then takes
+// up to 160 KB of LDS.
+static bool head_plan16(int64_t K, int* nst, int* waves) {
+  if (K % 32 != 0) return false;
+  const int64_t steps = K / 32;
+  for (int d = 1; d <= 16; ++d)
+    if (steps % d == 0 && steps / d <= 16) {
+      *nst = d;
+      *waves = (int)(steps / d);
+      return true;
+    }
+  return false;
+}
+static bool head_fits(int64_t K, int nterms, int mc, int waves, int mr) {
+  const int64_t xbytes = (int64_t)nterms * mc * K * 2;
+  const int64_t xpt = ((int64_t)nterms * mc * K / 8 + 64 * waves - 1) / (64 * waves);
+  return xbytes + (int64_t)waves * mr * 16 * 4 <= (mr == 4 ? 65536 : 160 * 1024) && xpt <= 8;
+}
+
 int w4l_head_rows(int64_t K, int nterms) {
   int nst, waves;
+  if (head_plan16(K, &nst, &waves))
+    for (int mc = 16; mc > 4; --mc)
+      if (head_fits(K, nterms, mc, waves, 16)) return mc;
   if (!head_plan(K, &nst, &waves)) return 0;
-  for (int mc = 4; mc >= 1; --mc) {
-    const int64_t xbytes = (int64_t)nterms * mc * K * 2;
-    const int64_t xpt = ((int64_t)nterms * mc * K / 8 + 64 * waves - 1) / (64 * waves);
-    if (xbytes + waves * 4 * 16 * 4 <= 65536 && xpt <= 8) return mc;
-  }
+  for (int mc = 4; mc >= 1; --mc)
+    if (head_fits(K, nterms, mc, waves, 4)) return mc;
   return 0;
 }
 
 hipError_t w4l_head_logits(const uint16_t* x_planes, int64_t xplane, int nterms, const uint16_t* e, float* logits,
                            int64_t M, int64_t V, int64_t K, float cap, hipStream_t st) {
-  int nst, waves;
-  if (!head_plan(K, &nst, &waves) || M < 1 || M > 4) return hipErrorInvalidValue;
+  // the 4-row form where it fits (M <= 4), else the 16-row form
+  int nst = 0, waves = 0, mr = 0;
+  if (M >= 1 && M <= 4 && head_plan(K, &nst, &waves) && head_fits(K, nterms, (int)M, waves, 4)) mr = 4;
+  else if (M >= 1 && M <= 16 && head_plan16(K, &nst, &waves) && head_fits(K, nterms, (int)M, waves, 16)) mr = 16;
+  if (!mr) return hipErrorInvalidValue;
   w4k::HeadArgs a{};
   a.x = x_planes;
   a.xplane = xplane;
@@ -252,9 +276,22 @@ hipError_t w4l_head_logits(const uint16_t* x_planes, int64_t xplane, int nterms,
   int xpt = 1;
   while (xpt < per) xpt *= 2;
   if (xpt > 8) return hipErrorInvalidValue;
-  const size_t lds = (size_t)nterms * M * K * 2 + (size_t)waves * 4 * 16 * 4;
+  const size_t lds = (size_t)nterms * M * K * 2 + (size_t)waves * mr * 16 * 4;
   const dim3 grid((unsigned)((V + 15) / 16)), block(64 * waves);
-#define W4_HEAD(NT_, NST_, XPT_) hipLaunchKernelGGL((w4k::head_logits_kernel<NT_, NST_, XPT_>), grid, block, lds, st, a)
+  hipError_t err = hipSuccess;
+#define W4_HEAD(NT_, NST_, XPT_)                                                                      \
+  do {                                                                                                \
+    if (mr == 16) {                                                                                   \
+      auto k = w4k::head_logits_kernel<NT_, NST_, XPT_, 16>;                                          \
+      if (lds > 65536 &&                                                                              \
+          (err = hipFuncSetAttribute(reinterpret_cast<const void*>(k),                                \
+                                     hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024)) != hipSuccess) \
+        return err;                                                                                   \
+      hipLaunchKernelGGL(k, grid, block, lds, st, a);                                                 \
+    } else {                                                                                          \
+      hipLaunchKernelGGL((w4k::head_logits_kernel<NT_, NST_, XPT_>), grid, block, lds, st, a);        \
+    }                                                                                                 \
+  } while (0)
 #define W4_HEAD_X(NT_, NST_)                  \
   switch (xpt) {                              \
     case 1: W4_HEAD(NT_, NST_, 1); break;     \

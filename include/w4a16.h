@@ -215,7 +215,8 @@ size_t w4a16_lm_head_workspace_size(int64_t M, int64_t V, int64_t K, int32_t x_d
  *   logits    f32 [M, V] output (the step returns it alongside the top-k).
  *   topk      0..64 with topk <= V and ceil(V / 4096) * topk <= 4096; 0 skips the top-k
  *             (top_values / top_indices may then be NULL).
- * The kernels read embed once per 4 rows of x (2 with f32 x): the decode head, M = 1.
+ * The kernels read embed once per launch of up to 16 rows of x at K = 3840 (5 with
+ * f32 x): the decode head (M = 1) and a batch of up to 16 sequences in one pass.
  */
 int w4a16_lm_head(const void *x, int32_t x_dtype, const uint16_t *embed, float *logits,
                   int64_t M, int64_t V, int64_t K, float softcap, int32_t topk,

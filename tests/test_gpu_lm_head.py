@@ -84,6 +84,10 @@ CASES = [
     (6, 1500, 3840, False, 30.0, 5),    # bf16 x, rows in chunks of 4
     (1, 777, 1536, False, 30.0, 0),     # logits only
     (1, 262144, 256, False, 30.0, 64),  # 64 candidates from 4096-logit slices
+    (16, 3000, 3840, False, 30.0, 5),   # one launch of 16 rows (16-row epilogue, 138 KB of LDS)
+    (11, 777, 1536, False, 0.0, 3),     # 11 rows in one launch, no softcap
+    (20, 600, 3840, False, 30.0, 4),    # 16 + 4 rows: the 16-row and the 4-row forms
+    (7, 900, 3840, True, 30.0, 5),      # f32 x: chunks of 5 + 2 rows
 ]
 
 
