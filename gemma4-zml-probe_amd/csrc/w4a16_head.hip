@@ -110,6 +110,87 @@ __global__ void __launch_bounds__(1024) head_logits_kernel(HeadArgs a) {
   }
 }
 
+// The same logits with a tile loop: each workgroup stages x once and walks
+// `per` consecutive 16-row tiles, the loads of tile t+1 in flight while tile t
+// computes (two register buffers, every load unconditional with the tile index
+// clamped so the wait counts stay exact).  x is then read from L2 once per
+// workgroup instead of once per tile: 16384 tiles re-reading a 123 KB x (16
+// rows at K = 3840) is 2 GB, as much as the embedding.
+template <int NT, int NST, int XPT, int MR>
+__global__ void __launch_bounds__(1024) head_loop_kernel(HeadArgs a, int per) {
+  extern __shared__ __attribute__((aligned(16))) uint16_t lds[];
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int nwaves = blockDim.x >> 6;
+  const int r = lane & 15, c = lane >> 4;
+  const int ntiles = (a.V + 15) >> 4;
+  const int t0 = (int)blockIdx.x * per;
+  const int tend = min(t0 + per, ntiles);
+
+  const int pv = (a.M * a.K) >> 3;
+  const int nvec = NT * pv;
+  const uint4* xsrc = reinterpret_cast<const uint4*>(a.x);
+  uint4 xv[XPT];
+  int xi[XPT];
+#pragma unroll
+  for (int i = 0; i < XPT; ++i) {
+    xi[i] = min((int)threadIdx.x + i * (int)blockDim.x, nvec - 1);
+    const int t = NT == 1 ? 0 : xi[i] / pv;
+    xv[i] = xsrc[t * (a.xplane >> 3) + (xi[i] - t * pv)];
+  }
+  uint4 wv[2][NST];
+  auto wload = [&](auto b_c, int tile) __attribute__((always_inline)) {
+    constexpr int b = decltype(b_c)::value;
+    const int n = min(min(tile, tend - 1) * 16 + r, a.V - 1);
+    const uint16_t* erow = a.e + (int64_t)n * a.K + wave * NST * 32 + 8 * c;
+#pragma unroll
+    for (int i = 0; i < NST; ++i) wv[b][i] = *reinterpret_cast<const uint4*>(erow + 32 * i);
+  };
+  wload(std::integral_constant<int, 0>{}, t0);
+  uint4* xdst = reinterpret_cast<uint4*>(lds);
+#pragma unroll
+  for (int i = 0; i < XPT; ++i) xdst[xi[i]] = xv[i];
+  __syncthreads();
+
+  const int plane = a.M * a.K;
+  const uint16_t* xrow = lds + min(r, a.M - 1) * a.K + wave * NST * 32 + 8 * c;
+  float* red = reinterpret_cast<float*>(lds + NT * plane);  // [waves][MR][16]
+  auto compute = [&](auto b_c, int tile) __attribute__((always_inline)) {
+    constexpr int b = decltype(b_c)::value;
+    floatx4 acc[1] = {floatx4{0.f, 0.f, 0.f, 0.f}};
+#pragma unroll
+    for (int i = 0; i < NST; ++i) {
+      const bf16x8 w = __builtin_bit_cast(bf16x8, wv[b][i]);
+#pragma unroll
+      for (int t = 0; t < NT; ++t) mfma_acc(acc[0], *reinterpret_cast<const bf16x8*>(xrow + t * plane + 32 * i), w);
+    }
+    mfma_drain<1>(acc);
+    if (MR == 16 || c == 0) {
+#pragma unroll
+      for (int i = 0; i < 4; ++i) red[(wave * MR + (MR == 16 ? 4 * c : 0) + i) * 16 + r] = acc[0][i];
+    }
+    __syncthreads();
+    for (int t = (int)threadIdx.x; t < 16 * MR; t += (int)blockDim.x) {
+      const int m = t >> 4, rr = t & 15;
+      const int nout = tile * 16 + rr;
+      if (tile < tend && m < a.M && nout < a.V) {
+        float v = 0.f;
+        for (int w = 0; w < nwaves; ++w) v += red[(w * MR + m) * 16 + rr];
+        if (a.cap > 0.f) v = tanhf(v * (1.0f / a.cap)) * a.cap;
+        if (v != v) v = __uint_as_float(0x7fc00000u);
+        a.logits[(int64_t)m * a.V + nout] = v;
+      }
+    }
+    __syncthreads();  // red is rewritten by the next tile
+  };
+  for (int t = t0; t < tend; t += 2) {
+    wload(std::integral_constant<int, 1>{}, t + 1);
+    compute(std::integral_constant<int, 0>{}, t);
+    wload(std::integral_constant<int, 0>{}, t + 2);
+    compute(std::integral_constant<int, 1>{}, t + 1);
+  }
+}
+
 // ---------------------------------------------------------------- top-k
 __device__ __forceinline__ uint32_t order_bits(float v) {
   const uint32_t u = __float_as_uint(v);
@@ -277,8 +358,54 @@ hipError_t w4l_head_logits(const uint16_t* x_planes, int64_t xplane, int nterms,
   while (xpt < per) xpt *= 2;
   if (xpt > 8) return hipErrorInvalidValue;
   const size_t lds = (size_t)nterms * M * K * 2 + (size_t)waves * mr * 16 * 4;
-  const dim3 grid((unsigned)((V + 15) / 16)), block(64 * waves);
   hipError_t err = hipSuccess;
+  // 16-row form: the tile loop, ~1 workgroup per CU (2 when x fits in 64 KB)
+  // each walking `per` tiles (at M = 16, V = 262144: 539 -> 415 us).  The 4-row
+  // form keeps one workgroup per tile, which measured faster there (M = 1: 322
+  // against 350 us).  W4A16_HEAD_LOOP=0/1 overrides it for tuning.
+  bool loop = mr == 16;
+  if (const char* ev = getenv("W4A16_HEAD_LOOP")) loop = atoi(ev) != 0;
+  if (loop) {
+    const int64_t ntiles = (V + 15) / 16;
+    int64_t nwg = lds > 65536 ? 256 : 512;
+    if (const char* e2 = getenv("W4A16_HEAD_WG")) nwg = atoll(e2);
+    if (nwg < 1) nwg = 1;
+    const int per = (int)((ntiles + nwg - 1) / nwg);
+    const dim3 grid((unsigned)((ntiles + per - 1) / per)), block(64 * waves);
+#define W4_HL(NT_, NST_, XPT_)                                                                       \
+  do {                                                                                               \
+    auto k = mr == 16 ? w4k::head_loop_kernel<NT_, NST_, XPT_, 16> : w4k::head_loop_kernel<NT_, NST_, XPT_, 4>; \
+    if (lds > 65536 &&                                                                               \
+        (err = hipFuncSetAttribute(reinterpret_cast<const void*>(k),                                 \
+                                   hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024)) != hipSuccess) \
+      return err;                                                                                    \
+    hipLaunchKernelGGL(k, grid, block, lds, st, a, per);                                             \
+  } while (0)
+#define W4_HL_X(NT_, NST_)                  \
+  switch (xpt) {                            \
+    case 1: W4_HL(NT_, NST_, 1); break;     \
+    case 2: W4_HL(NT_, NST_, 2); break;     \
+    case 4: W4_HL(NT_, NST_, 4); break;     \
+    default: W4_HL(NT_, NST_, 8); break;    \
+  }
+#define W4_HL_N(NT_)                                                                 \
+  switch (nst) {                                                                     \
+    case 1: W4_HL_X(NT_, 1); break;   case 2: W4_HL_X(NT_, 2); break;                \
+    case 3: W4_HL_X(NT_, 3); break;   case 4: W4_HL_X(NT_, 4); break;                \
+    case 5: W4_HL_X(NT_, 5); break;   case 6: W4_HL_X(NT_, 6); break;                \
+    case 7: W4_HL_X(NT_, 7); break;   case 8: W4_HL_X(NT_, 8); break;                \
+    case 9: W4_HL_X(NT_, 9); break;   case 10: W4_HL_X(NT_, 10); break;              \
+    case 11: W4_HL_X(NT_, 11); break; case 12: W4_HL_X(NT_, 12); break;              \
+    case 13: W4_HL_X(NT_, 13); break; case 14: W4_HL_X(NT_, 14); break;              \
+    case 15: W4_HL_X(NT_, 15); break; default: W4_HL_X(NT_, 16); break;              \
+  }
+    if (nterms == 1) { W4_HL_N(1) } else { W4_HL_N(3) }
+#undef W4_HL_N
+#undef W4_HL_X
+#undef W4_HL
+    return hipGetLastError();
+  }
+  const dim3 grid((unsigned)((V + 15) / 16)), block(64 * waves);
 #define W4_HEAD(NT_, NST_, XPT_)                                                                      \
   do {                                                                                                \
     if (mr == 16) {                                                                                   \
