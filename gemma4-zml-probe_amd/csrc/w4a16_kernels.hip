@@ -826,12 +826,16 @@ struct SkinnyArgs {
   int group_chunks;    // group / 32
   int groups_per_row;  // K / group
   int y_f32;
-  int nk;              // K / 256
+  int nk;              // chunks of 256 columns per K part (K / 256 / kq)
   // gate/up pair mode, as GemvArgs
   const uint32_t* pk2;
   const uint16_t* sc2;
   int pair_f;
   int bf16_dots;
+  // K split (grid.z = kq parts of nk chunks): kq > 1 writes f32 partial sums
+  // part[kq][M][N] (N in virtual rows in pair mode) for splitk_finalize_kernel
+  int kq;
+  float* part;
 };
 
 constexpr int SK_P = 4;  // weight prefetch depth (chunks); even, for the two-slot x ring
@@ -853,6 +857,7 @@ __global__ void __launch_bounds__(64 * NW) skinny_kernel(SkinnyArgs a) {
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int r = lane & 15, c = lane >> 4;
   const int m0 = blockIdx.y * (16 * MT);
+  const int kb = (int)blockIdx.z * a.nk;  // first chunk of this K part
   const uint32_t* pkrow;
   const uint16_t* scrow;
   weight_row(a.pk, a.sc, a.pk2, a.sc2, a.pair_f, (int)blockIdx.x * (16 * NW) + 16 * wave + r, a.N, a.K,
@@ -864,7 +869,7 @@ __global__ void __launch_bounds__(64 * NW) skinny_kernel(SkinnyArgs a) {
   uint32_t sv[P];
   auto wload = [&](auto slot_c, int k) __attribute__((always_inline)) {
     constexpr int slot = decltype(slot_c)::value;
-    const int g0 = (k * 4 + c) * 2;
+    const int g0 = ((kb + k) * 4 + c) * 2;
     wv[slot][0] = *reinterpret_cast<const uint4*>(pkrow + 4 * g0);
     wv[slot][1] = *reinterpret_cast<const uint4*>(pkrow + 4 * g0 + 4);
     if (G32) sv[slot] = *reinterpret_cast<const uint32_t*>(scrow + g0);
@@ -882,7 +887,7 @@ __global__ void __launch_bounds__(64 * NW) skinny_kernel(SkinnyArgs a) {
       const int v = (int)threadIdx.x + NTH * i;
       const int row = v >> 5, col = (v & 31) * 8;
       const int m = min(m0 + row, a.M - 1);
-      const u32x4 t = *reinterpret_cast<const u32x4*>(a.x + (int64_t)m * a.K + k * 256 + col);
+      const u32x4 t = *reinterpret_cast<const u32x4*>(a.x + (int64_t)m * a.K + (kb + k) * 256 + col);
       xr[4 * i] = t[0];
       xr[4 * i + 1] = t[1];
       xr[4 * i + 2] = t[2];
@@ -968,7 +973,18 @@ __global__ void __launch_bounds__(64 * NW) skinny_kernel(SkinnyArgs a) {
 
   // D layout: lane (n = r, c) holds D[m = 4c + i][n]
   const int nout = (int)blockIdx.x * (16 * NW) + 16 * wave + r;
-  if (a.pair_f) {
+  if (a.kq > 1) {
+    if (nout < a.N) {
+      float* pp = a.part + (int64_t)blockIdx.z * a.M * a.N + nout;
+#pragma unroll
+      for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          const int m = m0 + 16 * mt + 4 * c + i;
+          if (m < a.M) pp[(int64_t)m * a.N] = acc[mt][i];
+        }
+    }
+  } else if (a.pair_f) {
     // Lanes r and r ^ 8 hold gate and up of row f for the same m; per pair of
     // rows m, m + 1 the gate lane finishes m and the up lane m + 1 (all lanes
     // active here).
@@ -1760,12 +1776,17 @@ W4Plan w4l_plan(int64_t M, int64_t N, int64_t K, int nterms) {
   return p;
 }
 
+static hipError_t splitk_finalize_launch(const float* part, int kq, int64_t M, int64_t Nv, void* y, int y_f32,
+                                         const W4Pair* pair, hipStream_t st);
+
 bool w4l_skinny_ok(int64_t M, int64_t K, int nterms) {
   return nterms == 1 && M > 4 && K % 256 == 0;
 }
 
 hipError_t w4l_skinny(const uint16_t* x, const int32_t* pk, const uint16_t* sc, void* y, int y_f32,
-                      int64_t M, int64_t N, int64_t K, int32_t group, hipStream_t st, const W4Pair* pair) {
+                      int64_t M, int64_t N, int64_t K, int32_t group, hipStream_t st, const W4Pair* pair, int kq,
+                      float* part) {
+  if (kq < 1 || (K / 256) % kq != 0 || (kq > 1 && !part)) return hipErrorInvalidValue;
   w4k::SkinnyArgs a{};
   if (pair) {
     N = 16 * ((pair->F + 7) / 8);
@@ -1784,7 +1805,9 @@ hipError_t w4l_skinny(const uint16_t* x, const int32_t* pk, const uint16_t* sc, 
   a.group_chunks = group / 32;
   a.groups_per_row = (int)(K / group);
   a.y_f32 = y_f32;
-  a.nk = (int)(K / 256);
+  a.nk = (int)(K / 256 / kq);
+  a.kq = kq;
+  a.part = part;
   int mt = M <= 16 ? 1 : M <= 32 ? 2 : 4;
   // W4A16_SKINNY_MT=<1|2|4>: tuning override of the 16-row x tiles per workgroup
   if (const char* e = getenv("W4A16_SKINNY_MT")) {
@@ -1796,9 +1819,10 @@ hipError_t w4l_skinny(const uint16_t* x, const int32_t* pk, const uint16_t* sc, 
   // 36.6 -> 30.7 us; M = 16 / 32: 22.0 / 26.6 -> 19.8 / 23.1).  Smaller N keeps
   // four waves so the grid still fills the GPU.  W4A16_SKINNY_NW=<4|8> overrides
   // it for tuning.
-  int nw = ((N + 127) / 128) * ((M + 16 * mt - 1) / (16 * mt)) >= 240 ? 8 : 4;
+  int nw = ((N + 127) / 128) * ((M + 16 * mt - 1) / (16 * mt)) * kq >= 240 ? 8 : 4;
   if (const char* e = getenv("W4A16_SKINNY_NW")) nw = atoi(e) == 8 ? 8 : 4;
-  const dim3 grid((unsigned)((N + 16 * nw - 1) / (16 * nw)), (unsigned)((M + 16 * mt - 1) / (16 * mt))),
+  const dim3 grid((unsigned)((N + 16 * nw - 1) / (16 * nw)), (unsigned)((M + 16 * mt - 1) / (16 * mt)),
+                  (unsigned)kq),
       block(64 * nw);
   const bool g32 = group == 32;
 #define W4_SK(MT_, NW_)                                                                               \
@@ -1816,7 +1840,9 @@ hipError_t w4l_skinny(const uint16_t* x, const int32_t* pk, const uint16_t* sc, 
   else W4_SK_N(4);
 #undef W4_SK_N
 #undef W4_SK
-  return hipGetLastError();
+  hipError_t e = hipGetLastError();
+  if (e != hipSuccess || kq == 1) return e;
+  return splitk_finalize_launch(part, kq, M, N, y, y_f32, pair, st);
 }
 
 bool w4l_prefill_ok(int64_t M, int64_t K, int nterms) {
@@ -1899,53 +1925,102 @@ hipError_t w4l_prefill(const uint16_t* x, const int32_t* pk, const uint16_t* sc,
   return hipGetLastError();
 }
 
-// Split-K plan for the skinny regime (4 < M <= 64, bf16 x) when the skinny
-// kernel's grid (N / 64 workgroups) cannot fill the GPU: N < 16384 rows, and
-// M > 16 or K >= 8192 (measured on the 12B q/k/v/o/down shapes: at M <= 16 and
-// K = 3840 the one-pass kernel is as fast).  Workgroups of WS waves x 32 W rows
-// (256 rows for M > 32, 128 for M <= 32; x blocks of 64 / 32 rows) and kq K
-// parts, the smallest divisor of K / 64 (<= 16) that gives >= 240 workgroups,
-// else the largest.  Costs kq f32 partial planes and one finalize pass; 12B down
-// at M = 64 goes from 75 to 28 us.  W4A16_SPLITK=0 turns it off and
-// W4A16_PF_KQ=<q> forces the part count (tuning).
+// Split-K plan (bf16 x, M <= 64, N < 16384) for the shapes whose one-pass grid
+// cannot fill the GPU:
+//  - M <= 4 when x is too large for the decode GEMV's LDS (12B down at M = 3..4:
+//    21.3 -> 15.5 us), skinny form only;
+//  - 4 < M <= 16 when the 16-row GEMV does not take the shape (it is faster
+//    where it does: 12B q/k/v/o, E2B rows at M = 8 / 16) and K >= 8192 or
+//    N < 8192, i.e. the one-pass skinny grid (N / 64 workgroups) is under half
+//    the CUs (E2B down at M = 16: 16.7 -> 9.9 us; 12B full-layer q, N = 8192,
+//    stays one-pass);
+//  - 16 < M <= 64.
+// Two forms:
+//  - skinny (K % 256 == 0): the skinny kernel over kq parts of K, kq the largest
+//    divisor of K / 256 (<= 64) that keeps ceil(N / 64) * (x blocks) * kq <= 256
+//    workgroups (one per CU).  Measured on the 12B shapes, us: down M = 8 / 16 /
+//    32 / 64 23.2 / 23.7 / 23.8 / 27.5 -> 15.5 / 15.9 / 18.5 / 25.3; q, o, k/v at
+//    M = 32 15.4, 12.6, 12.7 -> 10.2, 10.3, 9.6 and at M = 64 20.2, 21.6, 17.3 ->
+//    13.4, 13.3, 11.4 (each against the prefill form).
+//  - prefill (otherwise, M > 4): workgroups of WS waves x 32 W rows (256 rows for
+//    M > 32, 128 for M <= 32; x blocks of 64 / 32 rows) and kq parts, the
+//    smallest divisor of K / 64 (<= 16) that gives >= 240 workgroups, else the
+//    largest.
+// Both cost kq f32 partial planes and one finalize pass.  W4A16_SPLITK=0 turns
+// the route off, W4A16_SPLITK_SKINNY=0 the skinny form, and W4A16_PF_KQ=<q>
+// forces the part count when it divides (tuning).
 namespace {
-bool splitk_plan(int64_t M, int64_t N, int64_t K, int nterms, int* ws, int* kq, int* mb) {
-  if (nterms != 1 || M <= 4 || M > 64 || K % 64 != 0 || N <= 0 || N >= 16384) return false;
-  if (M <= 16 && K < 8192) return false;
+struct SplitPlan {
+  bool skinny;
+  int kq;
+  int ws, mb;  // prefill form
+};
+bool splitk_plan(int64_t M, int64_t N, int64_t K, int nterms, SplitPlan* p) {
+  if (nterms != 1 || M < 1 || M > 64 || K % 64 != 0 || N <= 0 || N >= 16384) return false;
+  if (M <= 4 && (w4l_gemv_ok(M, K, nterms) || K % 256 != 0)) return false;
+  if (M > 4 && M <= 16 && (w4l_gemv16_ok(M, N, K, nterms) || (K < 8192 && N >= 8192))) return false;
   if (const char* e = getenv("W4A16_SPLITK"))
     if (atoi(e) == 0) return false;
-  *mb = M <= 32 ? 1 : 2;
-  *ws = *mb == 2 ? 8 : 4;
-  const int64_t tiles = (N + 32 * *ws - 1) / (32 * *ws);
+  int force = 0;
+  if (const char* e = getenv("W4A16_PF_KQ")) force = atoi(e);
+  bool try_skinny = K % 256 == 0;
+  if (const char* e = getenv("W4A16_SPLITK_SKINNY"))
+    if (atoi(e) == 0) try_skinny = false;
+  if (try_skinny) {
+    const int64_t nk = K / 256;
+    const int64_t mt = M <= 16 ? 1 : M <= 32 ? 2 : 4;
+    const int64_t per_part = ((N + 63) / 64) * ((M + 16 * mt - 1) / (16 * mt));
+    int q = 0;
+    if (force >= 2 && force <= 64 && nk % force == 0) q = force;
+    for (int c = 2; !force && c <= nk && c <= 64; ++c)
+      if (nk % c == 0 && per_part * c <= 256) q = c;
+    if (q >= 2) {
+      *p = SplitPlan{true, q, 0, 0};
+      return true;
+    }
+  }
+  const int mb = M <= 32 ? 1 : 2;
+  const int ws = mb == 2 ? 8 : 4;
+  const int64_t tiles = (N + 32 * ws - 1) / (32 * ws);
   const int64_t steps = K / 64;
   int q = 0;
-  if (const char* e = getenv("W4A16_PF_KQ")) {
-    const int v = atoi(e);
-    if (v >= 1 && v <= 16 && steps % v == 0) q = v;
-  }
+  if (force >= 1 && force <= 16 && steps % force == 0) q = force;
   for (int c = 2; !q && c <= 16; ++c)
     if (steps % c == 0 && tiles * c >= 240) q = c;
   if (!q) {
     for (int c = 16; c >= 2 && !q; --c)
       if (steps % c == 0) q = c;
   }
-  if (q < 2) return false;
-  *kq = q;
+  if (q < 2 || M <= 4) return false;
+  *p = SplitPlan{false, q, ws, mb};
   return true;
 }
 }  // namespace
 
+// Sum of the kq partial planes part[kq][M][Nv] into y (gate/up: gelu(g) * u).
+static hipError_t splitk_finalize_launch(const float* part, int kq, int64_t M, int64_t Nv, void* y, int y_f32,
+                                         const W4Pair* pair, hipStream_t st) {
+  const int64_t cols = pair ? pair->F : Nv;
+  const int64_t outs = (cols % 4 == 0 && Nv % 4 == 0) ? M * cols / 4 : M * cols;  // threads (4 outputs each when aligned)
+  const int block_f = 256;
+  hipLaunchKernelGGL(w4k::splitk_finalize_kernel, dim3(grid_for(outs, block_f)), dim3(block_f), 0, st, part, kq,
+                     (int)M, (int)Nv, y, y_f32, pair ? (int)pair->F : 0, pair ? pair->bf16_dots : 0);
+  return hipGetLastError();
+}
+
 size_t w4l_splitk_bytes(int64_t M, int64_t N, int64_t K, int nterms) {
-  int ws, kq, mb;
-  if (!splitk_plan(M, N, K, nterms, &ws, &kq, &mb)) return 0;
-  return (size_t)kq * (size_t)M * (size_t)N * sizeof(float);
+  SplitPlan p;
+  if (!splitk_plan(M, N, K, nterms, &p)) return 0;
+  return (size_t)p.kq * (size_t)M * (size_t)N * sizeof(float);
 }
 
 hipError_t w4l_splitk(const uint16_t* x, const int32_t* pk, const uint16_t* sc, void* y, int y_f32, int64_t M,
                       int64_t N, int64_t K, int32_t group, hipStream_t st, const W4Pair* pair, float* part) {
-  int ws, kq, mb;
   const int64_t Nv = pair ? 16 * ((pair->F + 7) / 8) : N;
-  if (!splitk_plan(M, Nv, K, 1, &ws, &kq, &mb)) return hipErrorInvalidValue;
+  SplitPlan p;
+  if (!splitk_plan(M, Nv, K, 1, &p)) return hipErrorInvalidValue;
+  if (p.skinny) return w4l_skinny(x, pk, sc, y, y_f32, M, N, K, group, st, pair, p.kq, part);
+  const int kq = p.kq, ws = p.ws, mb = p.mb;
   w4k::PrefillArgs a{};
   if (pair) {
     a.pk2 = reinterpret_cast<const uint32_t*>(pair->pk_up);
@@ -1980,12 +2055,7 @@ hipError_t w4l_splitk(const uint16_t* x, const int32_t* pk, const uint16_t* sc, 
 #undef W4_SKQ
   hipError_t e = hipGetLastError();
   if (e != hipSuccess) return e;
-  const int64_t cols = pair ? pair->F : N;
-  const int64_t outs = (cols % 4 == 0 && Nv % 4 == 0) ? M * cols / 4 : M * cols;  // threads (4 outputs each when aligned)
-  const int block_f = 256;
-  hipLaunchKernelGGL(w4k::splitk_finalize_kernel, dim3(grid_for(outs, block_f)), dim3(block_f), 0, st, part, kq,
-                     (int)M, (int)Nv, y, y_f32, pair ? (int)pair->F : 0, pair ? pair->bf16_dots : 0);
-  return hipGetLastError();
+  return splitk_finalize_launch(part, kq, M, Nv, y, y_f32, pair, st);
 }
 
 hipError_t w4l_linear(const uint16_t* x_planes, int nterms, const int32_t* pk, const uint16_t* sc,

@@ -44,9 +44,11 @@ hipError_t w4l_gemv(const uint16_t* x_planes, int nterms, const int32_t* pk, con
 
 // Skinny / prefill path (M > 4, bf16 x, K % 256 == 0).
 bool w4l_skinny_ok(int64_t M, int64_t K, int nterms);
+// kq > 1 splits K into kq parts (K / 256 divisible by kq) with f32 partials
+// part[kq][M][N] (virtual rows in pair mode) and a finalize launch.
 hipError_t w4l_skinny(const uint16_t* x, const int32_t* pk, const uint16_t* sc, void* y, int y_f32,
                       int64_t M, int64_t N, int64_t K, int32_t group, hipStream_t st,
-                      const W4Pair* pair = nullptr);
+                      const W4Pair* pair = nullptr, int kq = 1, float* part = nullptr);
 
 // Prefill path (M > 64, bf16 x, K % 64 == 0).
 bool w4l_prefill_ok(int64_t M, int64_t K, int nterms);
@@ -80,7 +82,7 @@ hipError_t w4l_fill_zero(void* p, int64_t bytes, hipStream_t st);
 hipError_t w4l_linear(const uint16_t* x_planes, int nterms, const int32_t* pk, const uint16_t* sc,
                       void* y, int y_f32, int64_t M, int64_t N, int64_t K, int32_t group,
                       hipStream_t st);
-// Split-K route of the skinny regime (bf16 x, 4 < M <= 64): bytes of f32 partial
+// Split-K route (bf16 x, M <= 64, shapes whose one-pass grid is small): bytes of f32 partial
 // sums it needs (0 when the shape does not take it) and the launch (main kernel
 // + finalize); with pair set, N is ignored and the output is h [M, F].
 size_t w4l_splitk_bytes(int64_t M, int64_t N, int64_t K, int nterms);

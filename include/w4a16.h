@@ -88,14 +88,16 @@ int w4a16_dequant(const int32_t *pk, const uint16_t *sc, uint16_t *w,
  * Bytes of device workspace w4a16_linear can use for (M, N, K, x_dtype).
  * x_dtype = W4A16_DTYPE_F32: 6 * M * K bytes (rounded up to 256) to hold the
  * three bf16 terms of x, required.
- * x_dtype = W4A16_DTYPE_BF16: nothing is required.  For 4 < M <= 64 on shapes
- * whose one-pass kernel cannot fill the GPU (N < 16384, K % 64 == 0, and M > 16
- * or K >= 8192: the 12B q/k/v/o/down rows) it is the size of kq f32 partial
- * planes, kq * M * N * 4 bytes rounded up to 256 with 2 <= kq <= 16 K parts;
- * given at least that much, the call splits K across workgroups and adds the
- * parts in a second launch in a fixed order (deterministic).  With less, or
- * NULL, it takes the one-pass route; both meet the same fp32 bound.  0
- * otherwise.
+ * x_dtype = W4A16_DTYPE_BF16: nothing is required.  For M <= 64 on shapes
+ * whose one-pass kernel cannot fill the GPU (N < 16384, K % 64 == 0, and: M > 16;
+ * or 4 < M <= 16 beyond the 16-row decode GEMV with K >= 8192 or N < 8192; or
+ * M <= 4 with K % 256 == 0 and x beyond the decode GEMV's 64 KiB of LDS -- the
+ * 12B q/k/v/o rows at M > 16, down at M >= 3, E2B down at M = 16) it is the size
+ * of kq f32 partial planes, kq * M * N * 4 bytes rounded up to 256 with
+ * 2 <= kq <= 64 K parts; given at least that much, the call splits K across
+ * workgroups and adds the parts in a second launch in a fixed order
+ * (deterministic).  With less, or NULL, it takes the one-pass route; both meet
+ * the same fp32 bound.  0 otherwise.
  */
 size_t w4a16_workspace_size(int64_t M, int64_t N, int64_t K, int32_t x_dtype);
 
@@ -157,10 +159,10 @@ enum {
  * 0 when a fused kernel takes the shape: bf16 x with K % 256 == 0 (any M) or
  * with M > 64 and K % 64 == 0 (every Gemma gate/up shape: K = 1536 or 3840);
  * f32 x in the decode GEMV (M <= 4, K % 256 == 0, within its LDS and register
- * limits).  Optional, added on top: bf16 x at 4 < M <= 64 takes the split-K
- * route of w4a16_linear over the 16 * ceil(F / 8) interleaved gate/up rows
- * when that row count is below 16384 (E2B: F = 6144 at M > 16), with the
- * activation applied when the parts are added.
+ * limits).  Optional, added on top: bf16 x takes the split-K route of
+ * w4a16_linear (same shape rules) over the 16 * ceil(F / 8) interleaved
+ * gate/up rows when that row count is below 16384 (E2B: F = 6144 at M > 16),
+ * with the activation applied when the parts are added.
  */
 size_t w4a16_gate_up_workspace_size(int64_t M, int64_t F, int64_t K, int32_t x_dtype);
 

@@ -93,20 +93,64 @@ def test_unpack_dequant_validation(L):
     assert L.w4a16_dequant(None, None, None, 0, 64, 32, None) == 0
 
 
+def gemv_ok(M, K):
+    """Decode GEMV: 1 <= M <= 4 with x and the reduction tile in 64 KiB of LDS."""
+    return 1 <= M <= 4 and M * K * 2 + 16 * 4 * 16 * 4 <= 65536
+
+
+def gemv16_ok(M, N, K):
+    """16-row GEMV (4 < M <= 16): steps of 256 columns, the fewest steps per wave
+    p <= 6 with steps / p <= 16 waves, at most 8 x vectors per thread, x whole in
+    160 KB of LDS with the reduction tile, and every tile's re-read of x under
+    40 MiB."""
+    if not (4 < M <= 16 and K % 256 == 0 and N > 0):
+        return False
+    steps = K // 256
+    nst = next((p for p in range(1, 7) if steps % p == 0 and steps // p <= 16), 0)
+    if not nst:
+        return False
+    waves = steps // nst
+    per = -(-(M * K // 8) // (64 * waves))
+    xpt = 1
+    while xpt < per:
+        xpt *= 2
+    if xpt > 8 or M * K * 2 + waves * 16 * 16 * 4 > 160 * 1024:
+        return False
+    return -(-N // 16) * M * K * 2 <= 40 << 20
+
+
 def splitk_bytes(M, N, K):
-    """Optional split-K workspace of a bf16 linear (partial sums): 4 < M <= 64,
-    N < 16384, K % 64 == 0, and M > 16 or K >= 8192; kq = the smallest divisor
-    q <= 16 of K / 64 with tiles * q >= 240 (tiles of 256 W rows at M > 32, 128
-    below), else the largest divisor <= 16."""
-    if not (4 < M <= 64 and 0 < N < 16384 and K % 64 == 0 and (M > 16 or K >= 8192)):
+    """Optional split-K workspace of a bf16 linear (kq f32 partial planes).  Taken
+    when N < 16384, K % 64 == 0 and: 16 < M <= 64; or 4 < M <= 16 outside the
+    16-row GEMV with K >= 8192 or N < 8192; or M <= 4 outside the decode GEMV
+    with K % 256 == 0.  Skinny form (K % 256 == 0): kq = the largest divisor
+    q <= 64 of K / 256 with ceil(N / 64) * (x blocks of 16, 32 or 64 rows) * q
+    <= 256.  Otherwise (M > 4) the 32x32 form: the smallest divisor q <= 16 of
+    K / 64 with tiles * q >= 240 (tiles of 256 W rows at M > 32, 128 below),
+    else the largest."""
+    if not (1 <= M <= 64 and 0 < N < 16384 and K % 64 == 0):
         return 0
-    tiles = -(-N // (256 if M > 32 else 128))
-    steps = K // 64
-    divs = [q for q in range(2, 17) if steps % q == 0]
-    if not divs:
+    if M <= 4 and (gemv_ok(M, K) or K % 256 != 0):
         return 0
-    fill = [q for q in divs if tiles * q >= 240]
-    q = fill[0] if fill else divs[-1]
+    if 4 < M <= 16 and (gemv16_ok(M, N, K) or (K < 8192 and N >= 8192)):
+        return 0
+    q = 0
+    if K % 256 == 0:
+        nk = K // 256
+        mt = 1 if M <= 16 else 2 if M <= 32 else 4
+        per_part = -(-N // 64) * -(-M // (16 * mt))
+        fits = [c for c in range(2, min(nk, 64) + 1) if nk % c == 0 and per_part * c <= 256]
+        q = fits[-1] if fits else 0
+    if not q:
+        if M <= 4:
+            return 0
+        tiles = -(-N // (256 if M > 32 else 128))
+        steps = K // 64
+        divs = [c for c in range(2, 17) if steps % c == 0]
+        if not divs:
+            return 0
+        fill = [c for c in divs if tiles * c >= 240]
+        q = fill[0] if fill else divs[-1]
     return -(-(q * M * N * 4) // 256) * 256
 
 
@@ -118,14 +162,19 @@ def test_workspace_size(L):
 
 
 @pytest.mark.parametrize("M,N,K,expect", [
-    (64, 3840, 15360, 16 * 64 * 3840 * 4),  # 12B down: 15 tiles x 16 parts
-    (8, 3840, 15360, 8 * 8 * 3840 * 4),     # 30 tiles of 128 rows x 8 parts
-    (64, 4096, 3840, 15 * 64 * 4096 * 4),   # 12B q: 16 tiles, 15 | 60 steps
-    (64, 2048, 3840, 15 * 64 * 2048 * 4),   # k/v: no divisor fills, the largest <= 16
-    (32, 12288, 1536, 3 * 32 * 12288 * 4),  # E2B gate/up rows at M = 32
-    (16, 4096, 3840, 0),                    # M <= 16 at K < 8192: one-pass skinny
+    (64, 3840, 15360, 4 * 64 * 3840 * 4),   # 12B down: 60 W blocks of 64 rows x 4 parts
+    (8, 3840, 15360, 4 * 8 * 3840 * 4),     # M = 8 at K >= 8192: 60 x 4
+    (64, 4096, 3840, 3 * 64 * 4096 * 4),    # 12B q: 64 blocks, 3 | 15 chunks
+    (64, 2048, 3840, 5 * 64 * 2048 * 4),    # k/v: 32 blocks x 5
+    (32, 12288, 1536, 3 * 32 * 12288 * 4),  # E2B gate/up rows at M = 32: 192 blocks, 32x32 form
+    (16, 1536, 6144, 8 * 16 * 1536 * 4),    # E2B down at M = 16: beyond the 16-row GEMV, 24 x 8
+    (4, 3840, 15360, 4 * 4 * 3840 * 4),     # M = 4: x beyond the decode GEMV's LDS
+    (24, 700, 1152, 604928),                # K % 256 != 0: 32x32 form, 9 parts (9 * 24 * 700 * 4 rounded up to 256)
+    (2, 3840, 15360, 0),                    # decode GEMV (x fits its LDS)
+    (16, 4096, 3840, 0),                    # 16-row GEMV
+    (8, 6144, 1536, 0),                     # 16-row GEMV (E2B gate/up rows)
+    (16, 8192, 3840, 0),                    # beyond the 16-row GEMV, N >= 8192 at K < 8192: one-pass skinny
     (64, 30720, 3840, 0),                   # the skinny grid fills the GPU
-    (4, 3840, 15360, 0),                    # decode GEMV
     (65, 3840, 15360, 0),                   # prefill
     (64, 3840, 15360 + 32, 0),              # K % 64 != 0
 ])

@@ -119,10 +119,11 @@ CASES = [
     (5, 33, 256, 32, False, False, False),      # 16-row GEMV pair mode
     (8, 6144, 1536, 32, False, True, False),    # 16-row GEMV pair mode: E2B gate/up at M = 8
     (16, 72, 1024, 64, False, False, True),     # 16-row GEMV pair mode, group 64, bf16 dots, h bf16
-    (17, 9, 512, 32, False, True, False),       # split-K, one real row in the second x block
-    (40, 129, 1280, 32, False, True, True),     # split-K, bf16 dots
-    (64, 200, 768, 128, False, True, False),    # split-K (400 virtual rows), group 128
-    (32, 6144, 1536, 32, False, True, False),   # split-K: E2B gate/up at M = 32
+    (17, 9, 512, 32, False, True, False),       # split-K (skinny form, 2 parts), one real row in the second x block
+    (40, 129, 1280, 32, False, True, True),     # split-K (skinny form, 5 parts), bf16 dots
+    (64, 200, 768, 128, False, True, False),    # split-K (skinny form, 400 virtual rows), group 128
+    (16, 1000, 6144, 32, False, False, False),  # split-K at M = 16 beyond the 16-row GEMV (8 parts), h bf16
+    (32, 6144, 1536, 32, False, True, False),   # split-K (prefill form): E2B gate/up at M = 32
     (65, 50, 64, 32, False, True, False),       # prefill
     (300, 130, 192, 64, False, False, False),   # prefill, h bf16
     (257, 17, 320, 32, False, True, True),      # prefill, bf16 dots

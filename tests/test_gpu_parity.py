@@ -301,17 +301,22 @@ def test_linear_gemv16_route(M, K, N):
 
 
 @pytest.mark.parametrize("M,K,N,step", [
-    (64, 15360, 3840, 13),  # 12B down at M = 64: 15 W tiles x 16 K parts
-    (8, 15360, 3840, 13),   # M = 8 at K >= 8192: 32-row x blocks, 8 parts
-    (40, 3840, 2048, 1),    # 12B k/v rows, partial last x block
-    (33, 4096, 1000, 1),    # ragged N (last W tile partial), 64-row x block with one real row in its second half
-    (20, 1536, 300, 1),     # small: K / 64 = 24 steps
+    (64, 15360, 3840, 13),  # 12B down at M = 64: skinny form, 60 W blocks x 4 K parts
+    (8, 15360, 3840, 13),   # M = 8 at K >= 8192: skinny form, 4 parts
+    (40, 3840, 2048, 1),    # 12B k/v rows, 64-row x block with 24 repeated rows, 5 parts
+    (33, 4096, 1000, 1),    # ragged N (last W tile partial), one real row in the x block's second half, 16 parts
+    (20, 1536, 300, 1),     # small: 6 parts of one 256-column chunk
+    (16, 6144, 1536, 5),    # E2B down at M = 16 (beyond the 16-row GEMV), 8 parts
+    (4, 15360, 520, 1),     # M = 4 with x beyond the decode GEMV's LDS: 20 parts, ragged N
+    (3, 12288, 256, 1),     # M = 3: 48 parts of one chunk
+    (24, 1152, 700, 1),     # prefill form: K % 256 != 0, 9 parts of 128 columns
 ])
 def test_linear_splitk_route(M, K, N, step):
-    """The split-K route (bf16 x, 4 < M <= 64, a skinny grid too small to fill the
-    GPU): the default call (the wrapper allocates the optional workspace) and the
-    one-pass route (no workspace) both meet the stated f32 tolerance against the
-    oracle on every `step`-th row n; bf16 outputs meet the bf16 bound."""
+    """The split-K route (bf16 x, M <= 64, a one-pass grid too small to fill the
+    GPU; skinny kernel over K parts, or the 32x32 kernel when K % 256 != 0): the
+    default call (the wrapper allocates the optional workspace) and the one-pass
+    route (no workspace) both meet the stated f32 tolerance against the oracle on
+    every `step`-th row n; bf16 outputs meet the bf16 bound."""
     say(f"split-K M={M} K={K} N={N}")
     assert w4a16.workspace_size(M, N, K, w4a16.DTYPE_BF16) > 0
     _, pk, sc = o.synth_weights(N, K, 1100 + N)
