@@ -1309,12 +1309,23 @@ __global__ void __launch_bounds__(256) splitk_finalize_kernel(const float* __res
       const float4* pv = reinterpret_cast<const float4*>(part + (int64_t)m * N + vc);
       float4 g = pv[0], u = make_float4(0.f, 0.f, 0.f, 0.f);
       if (pair_f) u = pv[2];  // + 8 floats
-      for (int q = 1; q < kq; ++q) {
-        const float4 t = pv[q * (plane / 4)];
-        g.x += t.x; g.y += t.y; g.z += t.z; g.w += t.w;
-        if (pair_f) {
-          const float4 w = pv[q * (plane / 4) + 2];
-          u.x += w.x; u.y += w.y; u.z += w.z; u.w += w.w;
+      // parts in batches of FB: the batch's loads are issued together (indices
+      // clamped in bounds), then added in q order
+      constexpr int FB = 8;
+      for (int q0 = 1; q0 < kq; q0 += FB) {
+        float4 t[FB], w[FB];
+#pragma unroll
+        for (int i = 0; i < FB; ++i) {
+          const int64_t o = (int64_t)min(q0 + i, kq - 1) * (plane / 4);
+          t[i] = pv[o];
+          if (pair_f) w[i] = pv[o + 2];
+        }
+#pragma unroll
+        for (int i = 0; i < FB; ++i) {
+          if (q0 + i < kq) {
+            g.x += t[i].x; g.y += t[i].y; g.z += t[i].z; g.w += t[i].w;
+            if (pair_f) { u.x += w[i].x; u.y += w[i].y; u.z += w[i].z; u.w += w[i].w; }
+          }
         }
       }
       if (pair_f) {
