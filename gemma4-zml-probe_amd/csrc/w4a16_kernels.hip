@@ -838,7 +838,7 @@ struct SkinnyArgs {
   float* part;
 };
 
-constexpr int SK_P = 4;  // weight prefetch depth (chunks); even, for the two-slot x ring
+constexpr int SK_P = 4;  // weight prefetch depth (chunks); even, for the two-slot x ring (8: 8-10 % slower)
 
 // NW waves of 16 W rows per workgroup (4 or 8): 8 halves the x traffic from L2
 // (x is staged once per 16 * NW rows of W).
@@ -908,10 +908,9 @@ __global__ void __launch_bounds__(64 * NW) skinny_kernel(SkinnyArgs a) {
   xvec_t xreg0, xreg1;
   xload(xreg0, 0);
   xload(xreg1, min(1, a.nk - 1));
-  wload(std::integral_constant<int, 0>{}, 0);
-  wload(std::integral_constant<int, 1>{}, min(1, a.nk - 1));
-  wload(std::integral_constant<int, 2>{}, min(2, a.nk - 1));
-  wload(std::integral_constant<int, 3>{}, min(3, a.nk - 1));
+  static_for<0, P>([&](auto i_c) __attribute__((always_inline)) {
+    wload(i_c, min((int)decltype(i_c)::value, a.nk - 1));
+  });
   xstore(xreg0, 0);
   __syncthreads();
 
@@ -961,15 +960,11 @@ __global__ void __launch_bounds__(64 * NW) skinny_kernel(SkinnyArgs a) {
     __syncthreads();
   };
   int k = 0;
-  for (; k + P <= a.nk; k += P) {
-    iter(k, std::integral_constant<int, 0>{});
-    iter(k + 1, std::integral_constant<int, 1>{});
-    iter(k + 2, std::integral_constant<int, 2>{});
-    iter(k + 3, std::integral_constant<int, 3>{});
-  }
-  if (k < a.nk) iter(k, std::integral_constant<int, 0>{});
-  if (k + 1 < a.nk) iter(k + 1, std::integral_constant<int, 1>{});
-  if (k + 2 < a.nk) iter(k + 2, std::integral_constant<int, 2>{});
+  for (; k + P <= a.nk; k += P)
+    static_for<0, P>([&](auto i_c) __attribute__((always_inline)) { iter(k + decltype(i_c)::value, i_c); });
+  static_for<0, P - 1>([&](auto i_c) __attribute__((always_inline)) {
+    if (k + decltype(i_c)::value < a.nk) iter(k + decltype(i_c)::value, i_c);
+  });
 
   // D layout: lane (n = r, c) holds D[m = 4c + i][n]
   const int nout = (int)blockIdx.x * (16 * NW) + 16 * wave + r;
