@@ -477,6 +477,44 @@ def test_graph_capture_replays_match_eager():
         del junk
 
 
+@pytest.mark.parametrize("M,K,N", [(8, 15360, 1000), (24, 1152, 700)])
+def test_splitk_graph_replays_match_eager(M, K, N):
+    """The split-K route (main kernel + finalize over the caller's workspace; the
+    skinny form with 15 parts, the 32x32 form with 9) captured in a HIP graph:
+    every replay equals the eager result bit for bit, since the parts are added
+    in a fixed order, with other eager work between the replays."""
+    say(f"split-K graph capture / replay M={M} K={K} N={N}")
+    _, pk, sc = o.synth_weights(N, K, 51)
+    pkd, scd = dev(pk), dev_u16(sc)
+    x = dev_u16(o.synth_x(M, K, 52))
+    nws = w4a16.workspace_size(M, N, K, w4a16.DTYPE_BF16)
+    assert nws > 0
+    ws = torch.empty(nws, dtype=torch.uint8, device="cuda")
+    y = torch.empty((M, N), dtype=torch.bfloat16, device="cuda")
+    ref = w4a16.linear(x, pkd, scd, out_dtype=torch.bfloat16, workspace=ws).clone()
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(s):
+        w4a16.linear(x, pkd, scd, out=y, workspace=ws)
+    torch.cuda.current_stream().wait_stream(s)
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        w4a16.linear(x, pkd, scd, out=y, workspace=ws)
+    for rep in range(4):
+        y.fill_(float("nan"))
+        ws.fill_(0xFF)  # the partial planes hold other data between replays
+        junk = w4a16.linear(x, pkd, scd, out_dtype=torch.float32)  # eager work between replays
+        torch.cuda.synchronize()
+        g.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(y.view(torch.int16), ref.view(torch.int16)), rep
+        del junk
+    w = o.dequant(pk, sc)
+    _, mag = o.matmul_f64(o.synth_x(M, K, 52), w)
+    check_bf16(host_u16(y), o.matmul_f32(o.synth_x(M, K, 52), w), mag, K)
+
+
 @pytest.mark.parametrize("K,N", [(3840, 512), (15360, 256), (4096, 64)])
 def test_gemv_stream_plans(K, N, monkeypatch):
     """The streaming GEMV under every (waves per tile, steps per chunk) plan the
