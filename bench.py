@@ -421,6 +421,8 @@ def main() -> int:
         cfgs += [(f"12B_{n}", 1, K, N) for n, K, N in LAYER_12B]
         # full-attention layers of the 12B (no v_proj): q 3840->8192, k 3840->512, o 8192->3840
         cfgs += [("12B_full_q", 1, 3840, 8192), ("12B_full_k", 1, 3840, 512), ("12B_full_o", 1, 8192, 3840)]
+        # E2B per-layer-embedding linears (engine.zig:659, 661, 723)
+        cfgs += [("E2B_ple_gate", 1, 1536, 256), ("E2B_ple_proj", 1, 256, 1536), ("E2B_plmp", 1, 1536, 8960)]
         cfgs += [(f"C4_M{M}", M, 3840, 30720) for M in (8, 16, 32, 64)]
         # configs[3] covers every config-2 weight at M = 8..64: the other linears of the layer
         cfgs += [(f"C4_{n}_M{M}", M, K, N) for M in (8, 16, 32, 64)

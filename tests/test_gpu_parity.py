@@ -232,6 +232,9 @@ C123 = {  # (K, N)
     "12B_kv": (3840, 2048), "12B_o": (4096, 3840),
     # 12B full-attention layers (g12.zig:139-166: no v_proj; q 3840->8192, k 3840->512, o 8192->3840)
     "12B_full_q": (3840, 8192), "12B_full_k": (3840, 512), "12B_full_o": (8192, 3840),
+    # E2B per-layer-embedding linears (engine.zig:659 gate 1536->256, :661 projection 256->1536,
+    # :723 per_layer_model_projection 1536->35*256)
+    "E2B_ple_gate": (1536, 256), "E2B_ple_proj": (256, 1536), "E2B_plmp": (1536, 8960),
 }
 
 
