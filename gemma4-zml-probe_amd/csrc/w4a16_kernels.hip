@@ -1284,6 +1284,166 @@ __global__ void __launch_bounds__(64 * WS * KS) prefill_kernel(PrefillArgs a) {
   });
 }
 
+// ---------------------------------------------------------------- prefill, W expanded into LDS
+// M > 64, bf16 x, K % 64 == 0.  A workgroup of 8 waves (two per SIMD) owns 256
+// rows of x and 256 rows of W and walks K in steps of 64 columns.  Per step every
+// thread expands one 16-byte packed vector (32 weights of one W row, one scale
+// group of 32), loaded P steps ahead, into the step's bf16 W tile in LDS, and the
+// x tile is staged beside it; both tiles are double buffered.  Wave (wm, wn)
+// multiplies x rows 128 wm .. +128 by W rows 64 wn .. +64 as 4 x 2 MFMA tiles of
+// 32x32, reading A and B fragments from LDS (rows of 72 halves: both read
+// patterns are conflict-free).  Each weight is still expanded once per 256 rows
+// of x, and each SIMD has a second wave to issue while one waits.
+template <bool G32>
+__global__ void __launch_bounds__(512) prefill_lds_kernel(PrefillArgs a) {
+  constexpr int P = 4;          // packed-weight ring depth (steps)
+  constexpr int RS = 72;        // LDS row stride (halves)
+  constexpr int TILE = 256 * RS;
+  extern __shared__ __attribute__((aligned(16))) uint16_t lds[];  // xs[2][256][RS] then ws[2][256][RS]
+  uint16_t* const xs = lds;
+  uint16_t* const ws = lds + 2 * TILE;
+  const int tid = (int)threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int wm = wave & 1, wn = wave >> 1;
+  const int l32 = lane & 31, h = lane >> 5;
+  const int bt = (int)blockIdx.x;
+  const int m0 = (bt % a.mblk) * 256;
+  const int n0 = (bt / a.mblk) * 256;
+  const int ns = a.ns;
+
+  // expansion: thread -> W row wr of the tile, 32-column half wh of the step
+  const int wr = tid >> 1, wh = tid & 1;
+  const uint32_t* pkrow;
+  const uint16_t* scrow;
+  weight_row(a.pk, a.sc, a.pk2, a.sc2, a.pair_f, n0 + wr, a.N, a.K, a.groups_per_row, pkrow, scrow);
+  uint4 wv[P];
+  uint32_t sv[P];
+  auto wload = [&](auto slot_c, int s) __attribute__((always_inline)) {
+    constexpr int slot = decltype(slot_c)::value;
+    const int g = 2 * s + wh;
+    wv[slot] = *reinterpret_cast<const uint4*>(pkrow + 4 * g);
+    sv[slot] = scrow[G32 ? g : g / a.group_chunks];
+  };
+  uint32_t kM = 0x000F000Fu, kO = 0x43004300u;
+  asm volatile("" : "+v"(kM), "+v"(kO));
+  auto expand = [&](auto slot_c, int buf) __attribute__((always_inline)) {
+    constexpr int slot = decltype(slot_c)::value;
+    const uint32_t shi = sv[slot] << 16;
+    const float cn = -136.0f * __uint_as_float(shi);
+    uint16_t* dst = ws + buf * TILE + wr * RS + 32 * wh;
+    const uint32_t w4[4] = {wv[slot].x, wv[slot].y, wv[slot].z, wv[slot].w};
+#pragma unroll
+    for (int j = 0; j < 4; ++j)
+      *reinterpret_cast<bf16x8*>(dst + 8 * j) = dequant8(w4[j], sv[slot], shi, cn, kM, kO);
+  };
+  // x tile [256][64]: vector v = tid + 512 i is row v / 8, columns 8 (v % 8) .. +8
+  u32x4 xr[4];
+  auto xload = [&](int s) __attribute__((always_inline)) {
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int v = tid + 512 * i;
+      const int m = min(m0 + (v >> 3), a.M - 1);
+      xr[i] = *reinterpret_cast<const u32x4*>(a.x + (int64_t)m * a.K + 64 * s + 8 * (v & 7));
+    }
+  };
+  auto xstore = [&](int buf) __attribute__((always_inline)) {
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int v = tid + 512 * i;
+      *reinterpret_cast<u32x4*>(xs + buf * TILE + (v >> 3) * RS + 8 * (v & 7)) = xr[i];
+    }
+  };
+
+  floatx16 acc[4][2];
+#pragma unroll
+  for (int i = 0; i < 4; ++i)
+#pragma unroll
+    for (int t = 0; t < 2; ++t) acc[i][t] = floatx16{};
+  auto compute = [&](int buf) __attribute__((always_inline)) {
+    const uint16_t* xb = xs + buf * TILE + (128 * wm + l32) * RS + 32 * h;
+    const uint16_t* wb = ws + buf * TILE + (64 * wn + l32) * RS + 32 * h;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      bf16x8 av[4], bv[2];
+#pragma unroll
+      for (int i = 0; i < 4; ++i) av[i] = *reinterpret_cast<const bf16x8*>(xb + 32 * i * RS + 8 * j);
+#pragma unroll
+      for (int t = 0; t < 2; ++t) bv[t] = *reinterpret_cast<const bf16x8*>(wb + 32 * t * RS + 8 * j);
+#pragma unroll
+      for (int i = 0; i < 4; ++i)
+#pragma unroll
+        for (int t = 0; t < 2; ++t) mfma32_acc(acc[i][t], av[i], bv[t]);
+    }
+  };
+
+  // prologue: packed steps 0..P-1 (slot k = step k), step 0 expanded and slot 0
+  // refilled with step P, x of step 0 staged
+  static_for<0, P>([&](auto i_c) __attribute__((always_inline)) {
+    wload(i_c, min((int)decltype(i_c)::value, ns - 1));
+  });
+  xload(0);
+  expand(std::integral_constant<int, 0>{}, 0);
+  wload(std::integral_constant<int, 0>{}, min(P, ns - 1));
+  xstore(0);
+  __syncthreads();
+  // step s (ring slot (s + 1) % P holds step s + 1): x of step s + 1 into registers,
+  // the MFMAs of step s, step s + 1 expanded into the other W buffer and its slot
+  // refilled with step s + 1 + P, x of step s + 1 into the other x buffer, barrier
+  auto iter = [&](int s, auto i_c) __attribute__((always_inline)) {
+    constexpr int i = decltype(i_c)::value;
+    xload(min(s + 1, ns - 1));
+    compute(s & 1);
+    expand(std::integral_constant<int, (i + 1) % P>{}, (s + 1) & 1);
+    wload(std::integral_constant<int, (i + 1) % P>{}, min(s + 1 + P, ns - 1));
+    xstore((s + 1) & 1);
+    __syncthreads();
+  };
+  int s = 0;
+  for (; s + P <= ns; s += P)
+    static_for<0, P>([&](auto i_c) __attribute__((always_inline)) { iter(s + decltype(i_c)::value, i_c); });
+  static_for<0, P - 1>([&](auto i_c) __attribute__((always_inline)) {
+    if (s + decltype(i_c)::value < ns) iter(s + decltype(i_c)::value, i_c);
+  });
+  // the last MFMAs must finish before their AGPRs are read (16-pass MFMA: >= 18 wait states)
+  asm volatile("s_nop 7\n\ts_nop 7\n\ts_nop 7\n\ts_nop 7" ::: "memory");
+
+  const int mb0 = m0 + 128 * wm;
+  static_for<0, 2>([&](auto t_c) __attribute__((always_inline)) {
+    constexpr int t = decltype(t_c)::value;
+    const int n = n0 + 64 * wn + 32 * t + l32;
+    if (a.pair_f) {
+      // lanes l and l ^ 8 hold gate and up of row f for the same m (as prefill_kernel)
+      const int f = ((n >> 4) << 3) | (l32 & 7);
+      const int up = (l32 >> 3) & 1;
+      static_for<0, 4>([&](auto i_c) __attribute__((always_inline)) {
+        constexpr int i = decltype(i_c)::value;
+        static_for<0, 8>([&](auto e_c) __attribute__((always_inline)) {
+          constexpr int e = 2 * decltype(e_c)::value;
+          const float p0 = lane_xor8(acc[i][t][e]), p1 = lane_xor8(acc[i][t][e + 1]);
+          const float g = up ? p1 : acc[i][t][e];
+          const float u = up ? acc[i][t][e + 1] : p0;
+          const int m = mb0 + 32 * i + 8 * (e >> 2) + 4 * h + (e & 3) + up;
+          if (f < a.pair_f && m < a.M) store_gelu_mul(a.y, a.y_f32, a.bf16_dots, (int64_t)m * a.pair_f + f, g, u);
+        });
+      });
+    } else if (n < a.N) {
+      static_for<0, 4>([&](auto i_c) __attribute__((always_inline)) {
+        constexpr int i = decltype(i_c)::value;
+#pragma unroll
+        for (int e = 0; e < 16; ++e) {
+          const int m = mb0 + 32 * i + 8 * (e >> 2) + 4 * h + (e & 3);
+          if (m < a.M) {
+            const float v = acc[i][t][e];
+            if (a.y_f32) reinterpret_cast<float*>(a.y)[(int64_t)m * a.N + n] = v;
+            else reinterpret_cast<uint16_t*>(a.y)[(int64_t)m * a.N + n] = (uint16_t)f32_to_bf16_rne(v);
+          }
+        }
+      });
+    }
+  });
+}
+
 // Split-K combine: y[m][n] = sum over q < kq of part[q][m][n] (f32 or bf16 out),
 // or in gate/up pair mode (pair_f = F) h[m][f] = gelu(g) * u with g and u the
 // sums of virtual rows ((f >> 3) << 4) | (f & 7) and that | 8.  The parts are
@@ -1911,6 +2071,23 @@ hipError_t w4l_prefill(const uint16_t* x, const int32_t* pk, const uint16_t* sc,
     else W4_PFS_M(2, 4);
 #undef W4_PFS_M
 #undef W4_PFS
+    return hipGetLastError();
+  }
+  // 256 x 256 tiles with W expanded into LDS (two waves per SIMD) when they
+  // still give >= 240 workgroups: measured on the 12B / E2B shapes, us, M = 512 /
+  // 1024 / 2048 / 4096 gate/up 167 / 327 / 536 / 1066 -> 133 / 257 / 510 / 1019,
+  // down at M = 4096 569 -> 457, full-layer q at M = 2048 167 -> 133; with fewer
+  // workgroups (12B down at M = 2048: 120) the one-wave-per-SIMD kernel below is
+  // faster (291 against 416).  W4A16_PF_LDS=0/1 overrides the choice (tuning).
+  bool lds_form = ((N + 255) / 256) * a.mblk >= 240;
+  if (const char* ev = getenv("W4A16_PF_LDS")) lds_form = atoi(ev) != 0;
+  if (mb == 8 && lds_form) {
+    const size_t lds = (size_t)4 * 256 * 72 * 2;
+    const dim3 grid((unsigned)(((N + 255) / 256) * a.mblk)), block(512);
+    auto k = group == 32 ? w4k::prefill_lds_kernel<true> : w4k::prefill_lds_kernel<false>;
+    hipError_t e = allow_big_lds(k, lds);
+    if (e != hipSuccess) return e;
+    hipLaunchKernelGGL(k, grid, block, lds, st, a);
     return hipGetLastError();
   }
   // two W blocks of 32 rows per wave when that still leaves two workgroups per CU

@@ -338,6 +338,24 @@ def test_linear_splitk_route(M, K, N, step):
     check_bf16(host_u16(yb)[:, rows], ref32, mag, K)
 
 
+@pytest.mark.parametrize("M,K,N,group", [(300, 640, 8000, 32), (257, 448, 700, 64), (2048, 128, 520, 128)])
+def test_prefill_lds_form(M, K, N, group, monkeypatch):
+    """The prefill kernel that expands W into LDS (256 x 256 tiles, 8 waves),
+    forced on shapes it would not take by itself: ragged M (x rows past M repeat
+    row M - 1) and N (the last W block partial), K steps that end in the ring's
+    tail (10 = 2 * 4 + 2, 7, 2), group sizes 32 / 64 / 128; every row m and n
+    against the oracle, f32 and bf16 outputs."""
+    monkeypatch.setenv("W4A16_PF_LDS", "1")
+    say(f"prefill LDS form M={M} K={K} N={N} group={group}")
+    _, pk, sc = o.synth_weights(N, K, 1500 + N, group=group)
+    x = o.synth_x(M, K, 1600 + M)
+    w = o.dequant(pk, sc, group)
+    ref32 = o.matmul_f32(x, w)
+    check_f32(gpu_linear(x, pk, sc, "f32", group=group), x, w, K, ref32)
+    _, mag = o.matmul_f64(x, w)
+    check_bf16(gpu_linear(x, pk, sc, "bf16", group=group), ref32, mag, K)
+
+
 @pytest.mark.parametrize("K,N", [(3840, 30720), (15360, 3840)])
 def test_linear_c5_prefill(K, N):
     """M = 2048; oracle on a sample of rows m and n."""
