@@ -1294,12 +1294,16 @@ __global__ void __launch_bounds__(64 * WS * KS) prefill_kernel(PrefillArgs a) {
 // 32x32, reading A and B fragments from LDS (rows of 72 halves: both read
 // patterns are conflict-free).  Each weight is still expanded once per 256 rows
 // of x, and each SIMD has a second wave to issue while one waits.
-template <bool G32>
+template <bool G32, int TN = 2>  // TN: W blocks of 32 rows per wave, 128 * TN W rows per workgroup
 __global__ void __launch_bounds__(512) prefill_lds_kernel(PrefillArgs a) {
   constexpr int P = 4;          // packed-weight ring depth (steps)
   constexpr int RS = 72;        // LDS row stride (halves)
   constexpr int TILE = 256 * RS;
-  extern __shared__ __attribute__((aligned(16))) uint16_t lds[];  // xs[2][256][RS] then ws[2][256][RS]
+  constexpr int BN = 128 * TN;
+  constexpr int WTILE = BN * RS;
+  constexpr int WPT = 2 * TN;       // packed words (8 weights each) a thread expands per step
+  constexpr int PPR = 8 / WPT;      // threads per W row
+  extern __shared__ __attribute__((aligned(16))) uint16_t lds[];  // xs[2][256][RS] then ws[2][BN][RS]
   uint16_t* const xs = lds;
   uint16_t* const ws = lds + 2 * TILE;
   const int tid = (int)threadIdx.x;
@@ -1309,20 +1313,27 @@ __global__ void __launch_bounds__(512) prefill_lds_kernel(PrefillArgs a) {
   const int l32 = lane & 31, h = lane >> 5;
   const int bt = (int)blockIdx.x;
   const int m0 = (bt % a.mblk) * 256;
-  const int n0 = (bt / a.mblk) * 256;
+  const int n0 = (bt / a.mblk) * BN;
   const int ns = a.ns;
 
-  // expansion: thread -> W row wr of the tile, 32-column half wh of the step
-  const int wr = tid >> 1, wh = tid & 1;
+  // expansion: thread -> W row wr of the tile, its part wh (8 * WPT columns) of the step
+  const int wr = tid / PPR, wh = tid % PPR;
   const uint32_t* pkrow;
   const uint16_t* scrow;
   weight_row(a.pk, a.sc, a.pk2, a.sc2, a.pair_f, n0 + wr, a.N, a.K, a.groups_per_row, pkrow, scrow);
-  uint4 wv[P];
+  uint32_t wv[P][WPT];
   uint32_t sv[P];
   auto wload = [&](auto slot_c, int s) __attribute__((always_inline)) {
     constexpr int slot = decltype(slot_c)::value;
-    const int g = 2 * s + wh;
-    wv[slot] = *reinterpret_cast<const uint4*>(pkrow + 4 * g);
+    const int w0 = 8 * s + WPT * wh;  // first packed word (column 8 * w0)
+    const int g = w0 >> 2;            // its 32-column scale group
+    if constexpr (WPT == 4) {
+      const uint4 t = *reinterpret_cast<const uint4*>(pkrow + w0);
+      wv[slot][0] = t.x; wv[slot][1] = t.y; wv[slot][2] = t.z; wv[slot][3] = t.w;
+    } else {
+      const uint2 t = *reinterpret_cast<const uint2*>(pkrow + w0);
+      wv[slot][0] = t.x; wv[slot][1] = t.y;
+    }
     sv[slot] = scrow[G32 ? g : g / a.group_chunks];
   };
   uint32_t kM = 0x000F000Fu, kO = 0x43004300u;
@@ -1331,11 +1342,10 @@ __global__ void __launch_bounds__(512) prefill_lds_kernel(PrefillArgs a) {
     constexpr int slot = decltype(slot_c)::value;
     const uint32_t shi = sv[slot] << 16;
     const float cn = -136.0f * __uint_as_float(shi);
-    uint16_t* dst = ws + buf * TILE + wr * RS + 32 * wh;
-    const uint32_t w4[4] = {wv[slot].x, wv[slot].y, wv[slot].z, wv[slot].w};
+    uint16_t* dst = ws + buf * WTILE + wr * RS + 8 * WPT * wh;
 #pragma unroll
-    for (int j = 0; j < 4; ++j)
-      *reinterpret_cast<bf16x8*>(dst + 8 * j) = dequant8(w4[j], sv[slot], shi, cn, kM, kO);
+    for (int j = 0; j < WPT; ++j)
+      *reinterpret_cast<bf16x8*>(dst + 8 * j) = dequant8(wv[slot][j], sv[slot], shi, cn, kM, kO);
   };
   // x tile [256][64]: vector v = tid + 512 i is row v / 8, columns 8 (v % 8) .. +8
   u32x4 xr[4];
@@ -1355,25 +1365,25 @@ __global__ void __launch_bounds__(512) prefill_lds_kernel(PrefillArgs a) {
     }
   };
 
-  floatx16 acc[4][2];
+  floatx16 acc[4][TN];
 #pragma unroll
   for (int i = 0; i < 4; ++i)
 #pragma unroll
-    for (int t = 0; t < 2; ++t) acc[i][t] = floatx16{};
+    for (int t = 0; t < TN; ++t) acc[i][t] = floatx16{};
   auto compute = [&](int buf) __attribute__((always_inline)) {
     const uint16_t* xb = xs + buf * TILE + (128 * wm + l32) * RS + 32 * h;
-    const uint16_t* wb = ws + buf * TILE + (64 * wn + l32) * RS + 32 * h;
+    const uint16_t* wb = ws + buf * WTILE + (32 * TN * wn + l32) * RS + 32 * h;
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
-      bf16x8 av[4], bv[2];
+      bf16x8 av[4], bv[TN];
 #pragma unroll
       for (int i = 0; i < 4; ++i) av[i] = *reinterpret_cast<const bf16x8*>(xb + 32 * i * RS + 8 * j);
 #pragma unroll
-      for (int t = 0; t < 2; ++t) bv[t] = *reinterpret_cast<const bf16x8*>(wb + 32 * t * RS + 8 * j);
+      for (int t = 0; t < TN; ++t) bv[t] = *reinterpret_cast<const bf16x8*>(wb + 32 * t * RS + 8 * j);
 #pragma unroll
       for (int i = 0; i < 4; ++i)
 #pragma unroll
-        for (int t = 0; t < 2; ++t) mfma32_acc(acc[i][t], av[i], bv[t]);
+        for (int t = 0; t < TN; ++t) mfma32_acc(acc[i][t], av[i], bv[t]);
     }
   };
 
@@ -1409,9 +1419,9 @@ __global__ void __launch_bounds__(512) prefill_lds_kernel(PrefillArgs a) {
   asm volatile("s_nop 7\n\ts_nop 7\n\ts_nop 7\n\ts_nop 7" ::: "memory");
 
   const int mb0 = m0 + 128 * wm;
-  static_for<0, 2>([&](auto t_c) __attribute__((always_inline)) {
+  static_for<0, TN>([&](auto t_c) __attribute__((always_inline)) {
     constexpr int t = decltype(t_c)::value;
-    const int n = n0 + 64 * wn + 32 * t + l32;
+    const int n = n0 + 32 * TN * wn + 32 * t + l32;
     if (a.pair_f) {
       // lanes l and l ^ 8 hold gate and up of row f for the same m (as prefill_kernel)
       const int f = ((n >> 4) << 3) | (l32 & 7);
@@ -2073,18 +2083,22 @@ hipError_t w4l_prefill(const uint16_t* x, const int32_t* pk, const uint16_t* sc,
 #undef W4_PFS
     return hipGetLastError();
   }
-  // 256 x 256 tiles with W expanded into LDS (two waves per SIMD) when they
-  // still give >= 240 workgroups: measured on the 12B / E2B shapes, us, M = 512 /
-  // 1024 / 2048 / 4096 gate/up 167 / 327 / 536 / 1066 -> 133 / 257 / 510 / 1019,
-  // down at M = 4096 569 -> 457, full-layer q at M = 2048 167 -> 133; with fewer
-  // workgroups (12B down at M = 2048: 120) the one-wave-per-SIMD kernel below is
-  // faster (291 against 416).  W4A16_PF_LDS=0/1 overrides the choice (tuning).
-  bool lds_form = ((N + 255) / 256) * a.mblk >= 240;
-  if (const char* ev = getenv("W4A16_PF_LDS")) lds_form = atoi(ev) != 0;
-  if (mb == 8 && lds_form) {
-    const size_t lds = (size_t)4 * 256 * 72 * 2;
-    const dim3 grid((unsigned)(((N + 255) / 256) * a.mblk)), block(512);
-    auto k = group == 32 ? w4k::prefill_lds_kernel<true> : w4k::prefill_lds_kernel<false>;
+  // W expanded into LDS, 8 waves (two per SIMD): 256 x 256 tiles when they still
+  // give >= 240 workgroups, else 256 x 128.  Measured on the 12B / E2B shapes, us,
+  // against the one-wave-per-SIMD kernel below: 256 x 256 gate/up at M = 512 /
+  // 1024 / 2048 / 4096 167 / 327 / 536 / 1066 -> 133 / 257 / 510 / 1019, down at
+  // M = 4096 569 -> 457; 256 x 128 down at M = 1024 / 2048 287 / 293 -> 249 / 279,
+  // full-layer o 163 -> 152, E2B down 124 -> 105 (the 256 x 256 tile gives those
+  // 60-120 workgroups and took 224-416).  W4A16_PF_LDS=0/1/2 overrides the choice
+  // (one-wave kernel / 128 / 256 W rows; tuning).
+  int lds_tn = ((N + 255) / 256) * a.mblk >= 240 ? 2 : 1;
+  if (const char* ev = getenv("W4A16_PF_LDS")) lds_tn = atoi(ev);
+  if (mb == 8 && (lds_tn == 1 || lds_tn == 2)) {
+    const int bn = 128 * lds_tn;
+    const size_t lds = (size_t)(2 * 256 + 2 * bn) * 72 * 2;
+    const dim3 grid((unsigned)(((N + bn - 1) / bn) * a.mblk)), block(512);
+    auto k = lds_tn == 2 ? (group == 32 ? w4k::prefill_lds_kernel<true, 2> : w4k::prefill_lds_kernel<false, 2>)
+                         : (group == 32 ? w4k::prefill_lds_kernel<true, 1> : w4k::prefill_lds_kernel<false, 1>);
     hipError_t e = allow_big_lds(k, lds);
     if (e != hipSuccess) return e;
     hipLaunchKernelGGL(k, grid, block, lds, st, a);
