@@ -1311,10 +1311,13 @@ __global__ void __launch_bounds__(512) prefill_lds_kernel(PrefillArgs a) {
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int wm = wave & 1, wn = wave >> 1;
   const int l32 = lane & 31, h = lane >> 5;
-  const int bt = (int)blockIdx.x;
+  // workgroup b: K part b % kq (kq = 1 without a split), then x block, then W block
+  const int kpart = (int)blockIdx.x % a.kq;
+  const int bt = (int)blockIdx.x / a.kq;
   const int m0 = (bt % a.mblk) * 256;
   const int n0 = (bt / a.mblk) * BN;
-  const int ns = a.ns;
+  const int ns = a.ns;               // steps of this part
+  const int sbase = kpart * a.ns;    // its first step
 
   // expansion: thread -> W row wr of the tile, its part wh (8 * WPT columns) of the step
   const int wr = tid / PPR, wh = tid % PPR;
@@ -1325,7 +1328,7 @@ __global__ void __launch_bounds__(512) prefill_lds_kernel(PrefillArgs a) {
   uint32_t sv[P];
   auto wload = [&](auto slot_c, int s) __attribute__((always_inline)) {
     constexpr int slot = decltype(slot_c)::value;
-    const int w0 = 8 * s + WPT * wh;  // first packed word (column 8 * w0)
+    const int w0 = 8 * (sbase + s) + WPT * wh;  // first packed word (column 8 * w0)
     const int g = w0 >> 2;            // its 32-column scale group
     if constexpr (WPT == 4) {
       const uint4 t = *reinterpret_cast<const uint4*>(pkrow + w0);
@@ -1354,7 +1357,7 @@ __global__ void __launch_bounds__(512) prefill_lds_kernel(PrefillArgs a) {
     for (int i = 0; i < 4; ++i) {
       const int v = tid + 512 * i;
       const int m = min(m0 + (v >> 3), a.M - 1);
-      xr[i] = *reinterpret_cast<const u32x4*>(a.x + (int64_t)m * a.K + 64 * s + 8 * (v & 7));
+      xr[i] = *reinterpret_cast<const u32x4*>(a.x + (int64_t)m * a.K + 64 * (sbase + s) + 8 * (v & 7));
     }
   };
   auto xstore = [&](int buf) __attribute__((always_inline)) {
@@ -1419,6 +1422,26 @@ __global__ void __launch_bounds__(512) prefill_lds_kernel(PrefillArgs a) {
   asm volatile("s_nop 7\n\ts_nop 7\n\ts_nop 7\n\ts_nop 7" ::: "memory");
 
   const int mb0 = m0 + 128 * wm;
+  if (a.kq > 1) {
+    // split K: this part's sums for every row m < M of every row n < N (the pair
+    // layout is resolved by the finalize kernel)
+    static_for<0, TN>([&](auto t_c) __attribute__((always_inline)) {
+      constexpr int t = decltype(t_c)::value;
+      const int n = n0 + 32 * TN * wn + 32 * t + l32;
+      if (n < a.N) {
+        float* pp = a.part + (int64_t)kpart * a.M * a.N + n;
+        static_for<0, 4>([&](auto i_c) __attribute__((always_inline)) {
+          constexpr int i = decltype(i_c)::value;
+#pragma unroll
+          for (int e = 0; e < 16; ++e) {
+            const int m = mb0 + 32 * i + 8 * (e >> 2) + 4 * h + (e & 3);
+            if (m < a.M) pp[(int64_t)m * a.N] = acc[i][t][e];
+          }
+        });
+      }
+    });
+    return;
+  }
   static_for<0, TN>([&](auto t_c) __attribute__((always_inline)) {
     constexpr int t = decltype(t_c)::value;
     const int n = n0 + 32 * TN * wn + 32 * t + l32;
@@ -2025,6 +2048,20 @@ bool w4l_prefill_ok(int64_t M, int64_t K, int nterms) {
   return nterms == 1 && M > 64 && K % 64 == 0;
 }
 
+// Launch of prefill_lds_kernel for filled PrefillArgs (mblk in 256-row x blocks,
+// ns steps per K part, kq parts): 128 * tn W rows per workgroup.
+static hipError_t prefill_lds_launch(const w4k::PrefillArgs& a, int tn, bool g32, hipStream_t st) {
+  const int bn = 128 * tn;
+  const size_t lds = (size_t)(2 * 256 + 2 * bn) * 72 * 2;
+  const dim3 grid((unsigned)((((int64_t)a.N + bn - 1) / bn) * a.mblk * a.kq)), block(512);
+  auto k = tn == 2 ? (g32 ? w4k::prefill_lds_kernel<true, 2> : w4k::prefill_lds_kernel<false, 2>)
+                   : (g32 ? w4k::prefill_lds_kernel<true, 1> : w4k::prefill_lds_kernel<false, 1>);
+  hipError_t e = allow_big_lds(k, lds);
+  if (e != hipSuccess) return e;
+  hipLaunchKernelGGL(k, grid, block, lds, st, a);
+  return hipGetLastError();
+}
+
 hipError_t w4l_prefill(const uint16_t* x, const int32_t* pk, const uint16_t* sc, void* y, int y_f32,
                        int64_t M, int64_t N, int64_t K, int32_t group, hipStream_t st, const W4Pair* pair) {
   w4k::PrefillArgs a{};
@@ -2093,17 +2130,7 @@ hipError_t w4l_prefill(const uint16_t* x, const int32_t* pk, const uint16_t* sc,
   // (one-wave kernel / 128 / 256 W rows; tuning).
   int lds_tn = ((N + 255) / 256) * a.mblk >= 240 ? 2 : 1;
   if (const char* ev = getenv("W4A16_PF_LDS")) lds_tn = atoi(ev);
-  if (mb == 8 && (lds_tn == 1 || lds_tn == 2)) {
-    const int bn = 128 * lds_tn;
-    const size_t lds = (size_t)(2 * 256 + 2 * bn) * 72 * 2;
-    const dim3 grid((unsigned)(((N + bn - 1) / bn) * a.mblk)), block(512);
-    auto k = lds_tn == 2 ? (group == 32 ? w4k::prefill_lds_kernel<true, 2> : w4k::prefill_lds_kernel<false, 2>)
-                         : (group == 32 ? w4k::prefill_lds_kernel<true, 1> : w4k::prefill_lds_kernel<false, 1>);
-    hipError_t e = allow_big_lds(k, lds);
-    if (e != hipSuccess) return e;
-    hipLaunchKernelGGL(k, grid, block, lds, st, a);
-    return hipGetLastError();
-  }
+  if (mb == 8 && (lds_tn == 1 || lds_tn == 2)) return prefill_lds_launch(a, lds_tn, group == 32, st);
   // two W blocks of 32 rows per wave when that still leaves two workgroups per CU
   const bool tn2 = mb == 8 && ((N + 255) / 256) * a.mblk >= 512;
   const int bn = tn2 ? 256 : 128;
@@ -2147,13 +2174,37 @@ hipError_t w4l_prefill(const uint16_t* x, const int32_t* pk, const uint16_t* sc,
 // the route off, W4A16_SPLITK_SKINNY=0 the skinny form, and W4A16_PF_KQ=<q>
 // forces the part count when it divides (tuning).
 namespace {
+enum SplitForm { SPLIT_SKINNY, SPLIT_PF32, SPLIT_LDS };
 struct SplitPlan {
-  bool skinny;
+  SplitForm form;
   int kq;
-  int ws, mb;  // prefill form
+  int ws, mb;  // 32x32 form
 };
 bool splitk_plan(int64_t M, int64_t N, int64_t K, int nterms, SplitPlan* p) {
-  if (nterms != 1 || M < 1 || M > 64 || K % 64 != 0 || N <= 0 || N >= 16384) return false;
+  if (nterms != 1 || M < 1 || K % 64 != 0 || N <= 0) return false;
+  if (M > 64) {
+    // prefill_lds_kernel with 256 x 128 tiles over kq K parts when its one-pass
+    // grid is under 240 workgroups: the smallest divisor of K / 64 (<= 16) that
+    // reaches 240, else the largest
+    if (const char* e = getenv("W4A16_SPLITK"))
+      if (atoi(e) == 0) return false;
+    const int64_t grid = ((N + 127) / 128) * ((M + 255) / 256);
+    if (grid >= 240) return false;
+    const int64_t steps = K / 64;
+    int q = 0;
+    if (const char* e = getenv("W4A16_PF_KQ")) {
+      const int v = atoi(e);
+      if (v >= 2 && v <= 16 && steps % v == 0) q = v;
+    }
+    for (int c = 2; !q && c <= 16; ++c)
+      if (steps % c == 0 && grid * c >= 240) q = c;
+    for (int c = 16; !q && c >= 2; --c)
+      if (steps % c == 0) q = c;
+    if (q < 2) return false;
+    *p = SplitPlan{SPLIT_LDS, q, 0, 0};
+    return true;
+  }
+  if (N >= 16384) return false;
   if (M <= 4 && (w4l_gemv_ok(M, K, nterms) || K % 256 != 0)) return false;
   if (M > 4 && M <= 16 && (w4l_gemv16_ok(M, N, K, nterms) || (K < 8192 && N >= 8192))) return false;
   if (const char* e = getenv("W4A16_SPLITK"))
@@ -2172,7 +2223,7 @@ bool splitk_plan(int64_t M, int64_t N, int64_t K, int nterms, SplitPlan* p) {
     for (int c = 2; !force && c <= nk && c <= 64; ++c)
       if (nk % c == 0 && per_part * c <= 256) q = c;
     if (q >= 2) {
-      *p = SplitPlan{true, q, 0, 0};
+      *p = SplitPlan{SPLIT_SKINNY, q, 0, 0};
       return true;
     }
   }
@@ -2189,7 +2240,7 @@ bool splitk_plan(int64_t M, int64_t N, int64_t K, int nterms, SplitPlan* p) {
       if (steps % c == 0) q = c;
   }
   if (q < 2 || M <= 4) return false;
-  *p = SplitPlan{false, q, ws, mb};
+  *p = SplitPlan{SPLIT_PF32, q, ws, mb};
   return true;
 }
 }  // namespace
@@ -2216,7 +2267,7 @@ hipError_t w4l_splitk(const uint16_t* x, const int32_t* pk, const uint16_t* sc, 
   const int64_t Nv = pair ? 16 * ((pair->F + 7) / 8) : N;
   SplitPlan p;
   if (!splitk_plan(M, Nv, K, 1, &p)) return hipErrorInvalidValue;
-  if (p.skinny) return w4l_skinny(x, pk, sc, y, y_f32, M, N, K, group, st, pair, p.kq, part);
+  if (p.form == SPLIT_SKINNY) return w4l_skinny(x, pk, sc, y, y_f32, M, N, K, group, st, pair, p.kq, part);
   const int kq = p.kq, ws = p.ws, mb = p.mb;
   w4k::PrefillArgs a{};
   if (pair) {
@@ -2236,9 +2287,15 @@ hipError_t w4l_splitk(const uint16_t* x, const int32_t* pk, const uint16_t* sc, 
   a.groups_per_row = (int)(K / group);
   a.y_f32 = y_f32;
   a.ns = (int)(K / 64 / kq);
-  a.mblk = (int)((M + 32 * mb - 1) / (32 * mb));
   a.kq = kq;
   a.part = part;
+  if (p.form == SPLIT_LDS) {
+    a.mblk = (int)((M + 255) / 256);
+    hipError_t e = prefill_lds_launch(a, 1, group == 32, st);
+    if (e != hipSuccess) return e;
+    return splitk_finalize_launch(part, kq, M, Nv, y, y_f32, pair, st);
+  }
+  a.mblk = (int)((M + 32 * mb - 1) / (32 * mb));
   const int bn = 32 * ws;
   const dim3 grid((unsigned)(((Nv + bn - 1) / bn) * a.mblk * kq)), block(64 * ws);
   const bool g32 = group == 32;

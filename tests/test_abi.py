@@ -120,14 +120,25 @@ def gemv16_ok(M, N, K):
 
 
 def splitk_bytes(M, N, K):
-    """Optional split-K workspace of a bf16 linear (kq f32 partial planes).  Taken
-    when N < 16384, K % 64 == 0 and: 16 < M <= 64; or 4 < M <= 16 outside the
+    """Optional split-K workspace of a bf16 linear (kq f32 partial planes).  Above
+    M = 64: when the LDS prefill kernel's grid (256 x 128 tiles) is under 240
+    workgroups, kq = the smallest divisor q <= 16 of K / 64 that reaches 240, else
+    the largest.  Else taken when N < 16384, K % 64 == 0 and: 16 < M <= 64; or 4 < M <= 16 outside the
     16-row GEMV with K >= 8192 or N < 8192; or M <= 4 outside the decode GEMV
     with K % 256 == 0.  Skinny form (K % 256 == 0): kq = the largest divisor
     q <= 64 of K / 256 with ceil(N / 64) * (x blocks of 16, 32 or 64 rows) * q
     <= 256.  Otherwise (M > 4) the 32x32 form: the smallest divisor q <= 16 of
     K / 64 with tiles * q >= 240 (tiles of 256 W rows at M > 32, 128 below),
     else the largest."""
+    if M > 64 and N > 0 and K % 64 == 0:
+        # 256 x 128 tiles of the LDS prefill kernel over K parts when its grid is under 240
+        grid = -(-N // 128) * -(-M // 256)
+        if grid >= 240:
+            return 0
+        divs = [c for c in range(2, 17) if (K // 64) % c == 0]
+        fill = [c for c in divs if grid * c >= 240]
+        q = fill[0] if fill else (divs[-1] if divs else 0)
+        return -(-(q * M * N * 4) // 256) * 256 if q else 0
     if not (1 <= M <= 64 and 0 < N < 16384 and K % 64 == 0):
         return 0
     if M <= 4 and (gemv_ok(M, K) or K % 256 != 0):
@@ -175,7 +186,11 @@ def test_workspace_size(L):
     (8, 6144, 1536, 0),                     # 16-row GEMV (E2B gate/up rows)
     (16, 8192, 3840, 0),                    # beyond the 16-row GEMV, N >= 8192 at K < 8192: one-pass skinny
     (64, 30720, 3840, 0),                   # the skinny grid fills the GPU
-    (65, 3840, 15360, 0),                   # prefill
+    (65, 3840, 15360, 8 * 65 * 3840 * 4),   # M > 64: LDS prefill form, 30 W blocks x 8 parts
+    (256, 3840, 15360, 8 * 256 * 3840 * 4), # the same at M = 256
+    (200, 1000, 4096, 16 * 200 * 1000 * 4), # 8 W blocks: no divisor of 64 fills, the largest <= 16
+    (2048, 3840, 15360, 0),                 # 240 workgroups one-pass: no split
+    (128, 30720, 3840, 0),                  # 240 W blocks
     (64, 3840, 15360 + 32, 0),              # K % 64 != 0
 ])
 def test_workspace_size_splitk(L, M, N, K, expect):

@@ -313,10 +313,14 @@ def test_linear_gemv16_route(M, K, N):
     (4, 15360, 520, 1),     # M = 4 with x beyond the decode GEMV's LDS: 20 parts, ragged N
     (3, 12288, 256, 1),     # M = 3: 48 parts of one chunk
     (24, 1152, 700, 1),     # prefill form: K % 256 != 0, 9 parts of 128 columns
+    (65, 15360, 3840, 13),  # M > 64: LDS prefill form, 30 W blocks x 8 parts, one real row in the second half
+    (200, 4096, 1000, 1),   # LDS form, ragged N, 16 parts
+    (300, 1152, 700, 3),    # LDS form, two x blocks, K % 256 != 0, 9 parts of 2 steps
 ])
 def test_linear_splitk_route(M, K, N, step):
-    """The split-K route (bf16 x, M <= 64, a one-pass grid too small to fill the
-    GPU; skinny kernel over K parts, or the 32x32 kernel when K % 256 != 0): the
+    """The split-K route (bf16 x, a one-pass grid too small to fill the GPU; the
+    skinny kernel over K parts, the 32x32 kernel when K % 256 != 0, and above
+    M = 64 the LDS prefill kernel): the
     default call (the wrapper allocates the optional workspace) and the one-pass
     route (no workspace) both meet the stated f32 tolerance against the oracle on
     every `step`-th row n; bf16 outputs meet the bf16 bound."""

@@ -181,7 +181,8 @@ def test_cpp_w4lin_linear_and_dequant_on_gpu(tool, tmp_path, M, out):
     x.tofile(tmp_path / "x.bin")
     rc, outp, err = run(tool, "linear", path, "blk", M, tmp_path / "x.bin", tmp_path / "y.bin", out)
     assert rc == 0, err
-    assert (json.loads(outp)["workspace"] > 0) == (M == 24)  # M = 24 at N = 96: the split-K route
+    # M = 24 and 70 at N = 96: the split-K route (skinny form, LDS prefill form)
+    assert (json.loads(outp)["workspace"] > 0) == (M in (24, 70))
     ref32 = o.matmul_f32(x, w)
     y64, mag = o.matmul_f64(x, w)
     gam = k * 2.0 ** -24 / (1 - k * 2.0 ** -24)
@@ -212,8 +213,9 @@ def test_cpp_mlp_rejects_mismatched_up(tool, tmp_path):
 @pytest.mark.gpu
 @pytest.mark.parametrize("M,out", [(1, "f32"), (3, "bf16"), (70, "f32"), (8, "bf16")])
 def test_cpp_gate_up_gelu_on_gpu(tool, tmp_path, M, out):
-    """gate_up_gelu through the C++ mirror (both fused routes and, at K = 320, M = 8, the
-    unfused one with tool-allocated workspace) against the oracle, with the bound of
+    """gate_up_gelu through the C++ mirror (the fused routes, the split-K route at M = 70
+    and, at K = 320, M = 8, the unfused one with tool-allocated workspace) against the
+    oracle, with the bound of
     tests/test_gpu_gate_up.py."""
     if not torch.cuda.is_available():
         pytest.skip("no GPU")
@@ -229,7 +231,9 @@ def test_cpp_gate_up_gelu_on_gpu(tool, tmp_path, M, out):
                         tmp_path / "h.bin", out)
     assert rc == 0, err
     ws = json.loads(outp)["workspace"]
-    assert (ws > 0) if M == 8 else (ws == 0)  # K = 320 at M = 8 takes the unfused route
+    # K = 320 at M = 8 takes the unfused route (required workspace); M = 70 the optional
+    # split-K route of the LDS prefill kernel (144 virtual rows: one workgroup one-pass)
+    assert (ws > 0) if M in (8, 70) else (ws == 0)
     pg = t["mlp.gate_proj.weight_packed"].numpy()
     sg = t["mlp.gate_proj.weight_scale"].view(torch.int16).numpy().view(np.uint16)
     pu = t["mlp.up_proj.weight_packed"].numpy()
