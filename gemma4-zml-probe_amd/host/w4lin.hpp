@@ -76,7 +76,7 @@ struct W4Lin {
   void linear(const uint16_t* x, uint16_t* y, int64_t m, hipStream_t stream) const;
   void linear(const uint16_t* x, float* y, int64_t m, hipStream_t stream) const;
   // The same with optional workspace: given workspace(m) bytes, batched shapes whose
-  // one-pass grid cannot fill the GPU (m <= 64 on the smaller rows) split K
+  // one-pass grid cannot fill the GPU (the smaller rows, m up to a few hundred) split K
   // across workgroups; 0 bytes or nullptr takes the one-pass route.
   size_t workspace(int64_t m) const;
   void linear(const uint16_t* x, uint16_t* y, int64_t m, void* workspace, size_t ws_bytes, hipStream_t stream) const;

@@ -168,10 +168,10 @@ def linear(x, pk, sc, out_dtype=None, group: int = GROUP, out=None, workspace=No
 
     x: bf16 or f32 [..., K] (leading dims flattened to M rows).  out_dtype
     bf16 (default for bf16 x) or f32 (default for f32 x).  f32 activations
-    need workspace; bf16 activations at M <= 64 on rows whose one-pass grid
-    cannot fill the GPU (12B down at M >= 3, q/k/v/o at M > 16) can use it for
-    the split-K route (allocated here when not given; pass an empty tensor to
-    take the one-pass route instead).
+    need workspace; bf16 activations on rows whose one-pass grid cannot fill
+    the GPU (12B down at M >= 3, q/k/v/o at M > 16, up to a few hundred rows)
+    can use it for the split-K route (allocated here when not given; pass an
+    empty tensor to take the one-pass route instead).
     """
     torch = _torch()
     _dev_check(x, pk, sc)

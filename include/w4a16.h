@@ -88,13 +88,14 @@ int w4a16_dequant(const int32_t *pk, const uint16_t *sc, uint16_t *w,
  * Bytes of device workspace w4a16_linear can use for (M, N, K, x_dtype).
  * x_dtype = W4A16_DTYPE_F32: 6 * M * K bytes (rounded up to 256) to hold the
  * three bf16 terms of x, required.
- * x_dtype = W4A16_DTYPE_BF16: nothing is required.  For M <= 64 on shapes
- * whose one-pass kernel cannot fill the GPU (N < 16384, K % 64 == 0, and: M > 16;
- * or 4 < M <= 16 beyond the 16-row decode GEMV with K >= 8192 or N < 8192; or
- * M <= 4 with K % 256 == 0 and x beyond the decode GEMV's 64 KiB of LDS -- the
- * 12B q/k/v/o rows at M > 16, down at M >= 3, E2B down at M = 16) it is the size
- * of kq f32 partial planes, kq * M * N * 4 bytes rounded up to 256 with
- * 2 <= kq <= 64 K parts; given at least that much, the call splits K across
+ * x_dtype = W4A16_DTYPE_BF16: nothing is required.  On shapes whose one-pass
+ * kernel cannot fill the GPU (K % 64 == 0, and: M > 64 with fewer than 240
+ * workgroups of 256 x 128; or N < 16384 and: 16 < M <= 64; 4 < M <= 16 beyond the
+ * 16-row decode GEMV with K >= 8192 or N < 8192; M <= 4 with K % 256 == 0 and x
+ * beyond the decode GEMV's 64 KiB of LDS -- the 12B q/k/v/o rows at M > 16, down
+ * at M >= 3 up to M = 1024, E2B down at M = 16) it is the size of kq f32 partial
+ * planes, kq * M * N * 4 bytes rounded up to 256 with 2 <= kq <= 64 K parts;
+ * given at least that much, the call splits K across
  * workgroups and adds the parts in a second launch in a fixed order
  * (deterministic).  With less, or NULL, it takes the one-pass route; both meet
  * the same fp32 bound.  0 otherwise.
