@@ -2184,12 +2184,15 @@ bool splitk_plan(int64_t M, int64_t N, int64_t K, int nterms, SplitPlan* p) {
   if (nterms != 1 || M < 1 || K % 64 != 0 || N <= 0) return false;
   if (M > 64) {
     // prefill_lds_kernel with 256 x 128 tiles over kq K parts when its one-pass
-    // grid is under 240 workgroups: the smallest divisor of K / 64 (<= 16) that
-    // reaches 240, else the largest
+    // grid is under 240 workgroups (N < 8192 at M <= 128): the smallest divisor of
+    // K / 64 (<= 16) that reaches 240, else the largest
     if (const char* e = getenv("W4A16_SPLITK"))
       if (atoi(e) == 0) return false;
     const int64_t grid = ((N + 127) / 128) * ((M + 255) / 256);
     if (grid >= 240) return false;
+    // up to 128 rows the one-pass kernel's 128-row x tiles waste no MFMAs, and with
+    // >= 64 workgroups it stays ahead (E2B gate/up rows at M = 128: 24.0 against 36.9)
+    if (M <= 128 && N >= 8192) return false;
     const int64_t steps = K / 64;
     int q = 0;
     if (const char* e = getenv("W4A16_PF_KQ")) {

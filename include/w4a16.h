@@ -90,15 +90,15 @@ int w4a16_dequant(const int32_t *pk, const uint16_t *sc, uint16_t *w,
  * three bf16 terms of x, required.
  * x_dtype = W4A16_DTYPE_BF16: nothing is required.  On shapes whose one-pass
  * kernel cannot fill the GPU (K % 64 == 0, and: M > 64 with fewer than 240
- * workgroups of 256 x 128; or N < 16384 and: 16 < M <= 64; 4 < M <= 16 beyond the
- * 16-row decode GEMV with K >= 8192 or N < 8192; M <= 4 with K % 256 == 0 and x
- * beyond the decode GEMV's 64 KiB of LDS -- the 12B q/k/v/o rows at M > 16, down
- * at M >= 3 up to M = 1024, E2B down at M = 16) it is the size of kq f32 partial
- * planes, kq * M * N * 4 bytes rounded up to 256 with 2 <= kq <= 64 K parts;
- * given at least that much, the call splits K across
- * workgroups and adds the parts in a second launch in a fixed order
- * (deterministic).  With less, or NULL, it takes the one-pass route; both meet
- * the same fp32 bound.  0 otherwise.
+ * workgroups of 256 x 128, and N < 8192 up to M = 128; or N < 16384 and:
+ * 16 < M <= 64; 4 < M <= 16 beyond the 16-row decode GEMV with K >= 8192 or
+ * N < 8192; M <= 4 with K % 256 == 0 and x beyond the decode GEMV's 64 KiB of
+ * LDS -- the 12B q/k/v/o rows at M > 16, down at M >= 3 up to M = 1024, E2B
+ * down at M = 16) it is the size of kq f32 partial planes, kq * M * N * 4 bytes
+ * rounded up to 256 with 2 <= kq <= 64 K parts; given at least that much, the
+ * call splits K across workgroups and adds the parts in a second launch in a
+ * fixed order (deterministic).  With less, or NULL, it takes the one-pass route;
+ * both meet the same fp32 bound.  0 otherwise.
  */
 size_t w4a16_workspace_size(int64_t M, int64_t N, int64_t K, int32_t x_dtype);
 
