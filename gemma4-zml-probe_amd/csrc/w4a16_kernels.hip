@@ -2184,8 +2184,10 @@ bool splitk_plan(int64_t M, int64_t N, int64_t K, int nterms, SplitPlan* p) {
   if (nterms != 1 || M < 1 || K % 64 != 0 || N <= 0) return false;
   if (M > 64) {
     // prefill_lds_kernel with 256 x 128 tiles over kq K parts when its one-pass
-    // grid is under 240 workgroups (N < 8192 at M <= 128): the smallest divisor of
-    // K / 64 (<= 16) that reaches 240, else the largest
+    // grid is under 240 workgroups (N < 8192 at M <= 128): the largest divisor of
+    // K / 64 (<= 16) that keeps the grid within 256 workgroups, one per CU (its LDS
+    // holds one workgroup per CU: q at M = 128 took 24.6 us with 192 workgroups
+    // against 31.9 with 320)
     if (const char* e = getenv("W4A16_SPLITK"))
       if (atoi(e) == 0) return false;
     const int64_t grid = ((N + 127) / 128) * ((M + 255) / 256);
@@ -2199,10 +2201,8 @@ bool splitk_plan(int64_t M, int64_t N, int64_t K, int nterms, SplitPlan* p) {
       const int v = atoi(e);
       if (v >= 2 && v <= 16 && steps % v == 0) q = v;
     }
-    for (int c = 2; !q && c <= 16; ++c)
-      if (steps % c == 0 && grid * c >= 240) q = c;
     for (int c = 16; !q && c >= 2; --c)
-      if (steps % c == 0) q = c;
+      if (steps % c == 0 && grid * c <= 256) q = c;
     if (q < 2) return false;
     *p = SplitPlan{SPLIT_LDS, q, 0, 0};
     return true;

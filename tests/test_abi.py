@@ -122,8 +122,8 @@ def gemv16_ok(M, N, K):
 def splitk_bytes(M, N, K):
     """Optional split-K workspace of a bf16 linear (kq f32 partial planes).  Above
     M = 64: when the LDS prefill kernel's grid (256 x 128 tiles) is under 240
-    workgroups (and N < 8192 up to M = 128), kq = the smallest divisor q <= 16 of
-    K / 64 that reaches 240, else
+    workgroups (and N < 8192 up to M = 128), kq = the largest divisor q <= 16 of
+    K / 64 with grid * q <= 256; else
     the largest.  Else taken when N < 16384, K % 64 == 0 and: 16 < M <= 64; or 4 < M <= 16 outside the
     16-row GEMV with K >= 8192 or N < 8192; or M <= 4 outside the decode GEMV
     with K % 256 == 0.  Skinny form (K % 256 == 0): kq = the largest divisor
@@ -136,9 +136,8 @@ def splitk_bytes(M, N, K):
         grid = -(-N // 128) * -(-M // 256)
         if grid >= 240 or (M <= 128 and N >= 8192):
             return 0
-        divs = [c for c in range(2, 17) if (K // 64) % c == 0]
-        fill = [c for c in divs if grid * c >= 240]
-        q = fill[0] if fill else (divs[-1] if divs else 0)
+        fits = [c for c in range(2, 17) if (K // 64) % c == 0 and grid * c <= 256]
+        q = fits[-1] if fits else 0
         return -(-(q * M * N * 4) // 256) * 256 if q else 0
     if not (1 <= M <= 64 and 0 < N < 16384 and K % 64 == 0):
         return 0
@@ -189,7 +188,8 @@ def test_workspace_size(L):
     (64, 30720, 3840, 0),                   # the skinny grid fills the GPU
     (65, 3840, 15360, 8 * 65 * 3840 * 4),   # M > 64: LDS prefill form, 30 W blocks x 8 parts
     (256, 3840, 15360, 8 * 256 * 3840 * 4), # the same at M = 256
-    (200, 1000, 4096, 16 * 200 * 1000 * 4), # 8 W blocks: no divisor of 64 fills, the largest <= 16
+    (200, 1000, 4096, 16 * 200 * 1000 * 4), # 8 W blocks x 16 parts
+    (128, 4096, 3840, 6 * 128 * 4096 * 4),  # q at M = 128: 32 W blocks x 6 parts (192 <= 256 workgroups)
     (2048, 3840, 15360, 0),                 # 240 workgroups one-pass: no split
     (128, 30720, 3840, 0),                  # 240 W blocks
     (128, 12288, 1536, 0),                  # M <= 128 with N >= 8192: the one-pass 128-row tiles
