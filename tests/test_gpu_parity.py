@@ -502,10 +502,11 @@ def test_graph_capture_replays_match_eager():
         del junk
 
 
-@pytest.mark.parametrize("M,K,N", [(8, 15360, 1000), (24, 1152, 700)])
+@pytest.mark.parametrize("M,K,N", [(8, 15360, 1000), (24, 1152, 700), (100, 2048, 700)])
 def test_splitk_graph_replays_match_eager(M, K, N):
     """The split-K route (main kernel + finalize over the caller's workspace; the
-    skinny form with 15 parts, the 32x32 form with 9) captured in a HIP graph:
+    skinny form with 15 parts, the 32x32 form with 9, the LDS prefill form with 16)
+    captured in a HIP graph:
     every replay equals the eager result bit for bit, since the parts are added
     in a fixed order, with other eager work between the replays."""
     say(f"split-K graph capture / replay M={M} K={K} N={N}")
