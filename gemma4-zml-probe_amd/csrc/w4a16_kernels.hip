@@ -2184,7 +2184,7 @@ bool splitk_plan(int64_t M, int64_t N, int64_t K, int nterms, SplitPlan* p) {
   if (nterms != 1 || M < 1 || K % 64 != 0 || N <= 0) return false;
   if (M > 64) {
     // prefill_lds_kernel with 256 x 128 tiles over kq K parts when its one-pass
-    // grid is under 240 workgroups (N < 8192 at M <= 128): the largest divisor of
+    // grid is under 240 workgroups (N <= 8192 at M <= 128): the largest divisor of
     // K / 64 (<= 16) that keeps the grid within 256 workgroups, one per CU (its LDS
     // holds one workgroup per CU: q at M = 128 took 24.6 us with 192 workgroups
     // against 31.9 with 320)
@@ -2193,8 +2193,9 @@ bool splitk_plan(int64_t M, int64_t N, int64_t K, int nterms, SplitPlan* p) {
     const int64_t grid = ((N + 127) / 128) * ((M + 255) / 256);
     if (grid >= 240) return false;
     // up to 128 rows the one-pass kernel's 128-row x tiles waste no MFMAs, and with
-    // >= 64 workgroups it stays ahead (E2B gate/up rows at M = 128: 24.0 against 36.9)
-    if (M <= 128 && N >= 8192) return false;
+    // 96 workgroups it stays ahead (E2B gate/up rows at M = 128: 24.0 against 36.9;
+    // with 64, full-layer q, the split wins: 32.3 against 49.8)
+    if (M <= 128 && N > 8192) return false;
     const int64_t steps = K / 64;
     int q = 0;
     if (const char* e = getenv("W4A16_PF_KQ")) {

@@ -90,7 +90,7 @@ int w4a16_dequant(const int32_t *pk, const uint16_t *sc, uint16_t *w,
  * three bf16 terms of x, required.
  * x_dtype = W4A16_DTYPE_BF16: nothing is required.  On shapes whose one-pass
  * kernel cannot fill the GPU (K % 64 == 0, and: M > 64 with fewer than 240
- * workgroups of 256 x 128, and N < 8192 up to M = 128; or N < 16384 and:
+ * workgroups of 256 x 128, and N <= 8192 up to M = 128; or N < 16384 and:
  * 16 < M <= 64; 4 < M <= 16 beyond the 16-row decode GEMV with K >= 8192 or
  * N < 8192; M <= 4 with K % 256 == 0 and x beyond the decode GEMV's 64 KiB of
  * LDS -- the 12B q/k/v/o rows at M > 16, down at M >= 3 up to M = 1024, E2B

@@ -122,7 +122,7 @@ def gemv16_ok(M, N, K):
 def splitk_bytes(M, N, K):
     """Optional split-K workspace of a bf16 linear (kq f32 partial planes).  Above
     M = 64: when the LDS prefill kernel's grid (256 x 128 tiles) is under 240
-    workgroups (and N < 8192 up to M = 128), kq = the largest divisor q <= 16 of
+    workgroups (and N <= 8192 up to M = 128), kq = the largest divisor q <= 16 of
     K / 64 with grid * q <= 256; else
     the largest.  Else taken when N < 16384, K % 64 == 0 and: 16 < M <= 64; or 4 < M <= 16 outside the
     16-row GEMV with K >= 8192 or N < 8192; or M <= 4 outside the decode GEMV
@@ -134,7 +134,7 @@ def splitk_bytes(M, N, K):
     if M > 64 and N > 0 and K % 64 == 0:
         # 256 x 128 tiles of the LDS prefill kernel over K parts when its grid is under 240
         grid = -(-N // 128) * -(-M // 256)
-        if grid >= 240 or (M <= 128 and N >= 8192):
+        if grid >= 240 or (M <= 128 and N > 8192):
             return 0
         fits = [c for c in range(2, 17) if (K // 64) % c == 0 and grid * c <= 256]
         q = fits[-1] if fits else 0
@@ -192,7 +192,8 @@ def test_workspace_size(L):
     (128, 4096, 3840, 6 * 128 * 4096 * 4),  # q at M = 128: 32 W blocks x 6 parts (192 <= 256 workgroups)
     (2048, 3840, 15360, 0),                 # 240 workgroups one-pass: no split
     (128, 30720, 3840, 0),                  # 240 W blocks
-    (128, 12288, 1536, 0),                  # M <= 128 with N >= 8192: the one-pass 128-row tiles
+    (128, 12288, 1536, 0),                  # M <= 128 with N > 8192: the one-pass 128-row tiles
+    (128, 8192, 3840, 4 * 128 * 8192 * 4),  # full-layer q at M = 128: 64 W blocks x 4 parts
     (64, 3840, 15360 + 32, 0),              # K % 64 != 0
 ])
 def test_workspace_size_splitk(L, M, N, K, expect):
