@@ -215,9 +215,20 @@ int w4a16_linear_group(const void* x, int32_t x_dtype, int32_t n, const int32_t*
   for (int j = 0; j < n; ++j) ntot += 16 * ((N[j] + 15) / 16);
   if (w4l_group_fused(M, ntot, K, nterms))
     return hip_status(w4l_gemv_group(planes, nterms, n, pk, sc, y, N, y_f32, M, K, group, st), fn);
-  for (int j = 0; j < n; ++j)
-    if (N[j] && (rc = hip_status(w4l_linear(planes, nterms, pk[j], sc[j], y[j], y_f32, M, N[j], K, group, st), fn)))
-      return rc;
+  // one launch each; with bf16 x and enough workspace a member takes the split-K
+  // route as w4a16_linear would (the members run in stream order, so they share
+  // the workspace one after another)
+  for (int j = 0; j < n; ++j) {
+    if (!N[j]) continue;
+    const size_t sk = nterms == 1 && workspace != nullptr ? splitk_bytes(M, N[j], K, x_dtype) : 0;
+    if (sk && ws_bytes >= sk)
+      rc = hip_status(w4l_splitk(planes, pk[j], sc[j], y[j], y_f32, M, N[j], K, group, st, nullptr,
+                                 static_cast<float*>(workspace)),
+                      fn);
+    else
+      rc = hip_status(w4l_linear(planes, nterms, pk[j], sc[j], y[j], y_f32, M, N[j], K, group, st), fn);
+    if (rc) return rc;
+  }
   return W4A16_OK;
 }
 

@@ -161,6 +161,17 @@ void gate_up_gelu(const W4Lin& gate, const W4Lin& up, const uint16_t* x, float* 
 
 void linear_group(const std::vector<W4Lin>& lins, const uint16_t* x, const std::vector<uint16_t*>& ys, int64_t m,
                   hipStream_t stream) {
+  linear_group(lins, x, ys, m, nullptr, 0, stream);
+}
+
+size_t linear_group_workspace(const std::vector<W4Lin>& lins, int64_t m) {
+  size_t ws = 0;
+  for (const W4Lin& lin : lins) ws = std::max(ws, lin.workspace(m));
+  return ws;
+}
+
+void linear_group(const std::vector<W4Lin>& lins, const uint16_t* x, const std::vector<uint16_t*>& ys, int64_t m,
+                  void* workspace, size_t ws_bytes, hipStream_t stream) {
   if (lins.empty() || lins.size() > 4 || ys.size() != lins.size())
     throw Error(W4A16_EINVAL_ARG, "linear_group: 1 to 4 linears, one output each");
   const int32_t* pk[4];
@@ -176,7 +187,7 @@ void linear_group(const std::vector<W4Lin>& lins, const uint16_t* x, const std::
     n[j] = lins[j].n;
   }
   check(w4a16_linear_group(x, W4A16_DTYPE_BF16, (int32_t)lins.size(), pk, sc, y, n, W4A16_DTYPE_BF16, m,
-                           lins[0].k, lins[0].group, 0, nullptr, 0, stream),
+                           lins[0].k, lins[0].group, 0, workspace, ws_bytes, stream),
         "linear_group");
 }
 

@@ -102,6 +102,12 @@ void gate_up_gelu(const W4Lin& gate, const W4Lin& up, const uint16_t* x, float* 
 // x . lins[j].toW()^T, one launch at decode; 1..4 linears with the same k and group.
 void linear_group(const std::vector<W4Lin>& lins, const uint16_t* x, const std::vector<uint16_t*>& ys, int64_t m,
                   hipStream_t stream);
+// The same with optional workspace: given linear_group_workspace(lins, m) bytes (the
+// largest member's W4Lin::workspace), members that run as their own launch take the
+// split-K route; 0 bytes or nullptr keeps them one-pass.
+size_t linear_group_workspace(const std::vector<W4Lin>& lins, int64_t m);
+void linear_group(const std::vector<W4Lin>& lins, const uint16_t* x, const std::vector<uint16_t*>& ys, int64_t m,
+                  void* workspace, size_t ws_bytes, hipStream_t stream);
 
 // The decode head (engine.zig:765-766) and its topK (gemma4_g12auto.zig:1532): logits[m, v] =
 // softcap * tanh(x . embed^T / softcap) (f32), top-k values (descending, ties by index) and

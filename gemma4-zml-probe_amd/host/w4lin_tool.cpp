@@ -193,7 +193,11 @@ int cmd_qkv(int argc, char** argv) {
     hip_ok(hipMalloc(&p, std::max<size_t>((size_t)(M * lin.n * 2), 16)), "hipMalloc y");
     ys.push_back(static_cast<uint16_t*>(p));
   }
-  w4::linear_group(lins, static_cast<const uint16_t*>(dx), ys, M, nullptr);
+  const size_t ws = w4::linear_group_workspace(lins, M);  // optional: split-K members
+  void* dws = nullptr;
+  if (ws) hip_ok(hipMalloc(&dws, ws), "hipMalloc workspace");
+  w4::linear_group(lins, static_cast<const uint16_t*>(dx), ys, M, dws, ws, nullptr);
+  if (dws) (void)hipFree(dws);
   for (size_t i = 0; i < lins.size(); ++i) {
     std::vector<char> h((size_t)(M * lins[i].n * 2));
     hip_ok(hipMemcpy(h.data(), ys[i], h.size(), hipMemcpyDeviceToHost), "copy y");
@@ -201,7 +205,8 @@ int cmd_qkv(int argc, char** argv) {
     (void)hipFree(ys[i]);
   }
   (void)hipFree(dx);
-  std::printf("{\"layer\": %d, \"linears\": %zu, \"M\": %lld}\n", j, lins.size(), (long long)M);
+  std::printf("{\"layer\": %d, \"linears\": %zu, \"M\": %lld, \"workspace\": %zu}\n", j, lins.size(),
+              (long long)M, ws);
   return 0;
 }
 

@@ -215,7 +215,9 @@ def linear(x, pk, sc, out_dtype=None, group: int = GROUP, out=None, workspace=No
 
 def linear_group(x, lins, out_dtype=None, outs=None, workspace=None):
     """[x . lin.toW()^T for lin in lins]: 1 to 4 linears that read the same x (q, k, v at
-    engine.zig:552,571,583), one launch at decode.  Each output equals linear(x, lin)."""
+    engine.zig:552,571,583), one launch at decode.  Each output equals linear(x, lin);
+    above the fused sizes the members take the split-K route with the workspace
+    (allocated here when not given; an empty tensor keeps them one-pass)."""
     torch = _torch()
     if not 1 <= len(lins) <= 4:
         raise W4A16Error(EINVAL_ARG, "linear_group takes 1 to 4 linears")
@@ -244,11 +246,12 @@ def linear_group(x, lins, out_dtype=None, outs=None, workspace=None):
         if o_.dtype != out_dtype or o_.numel() != M * lin.out_features:
             raise W4A16Error(EINVAL_SHAPE, "outs must match the linears' [M, N] and one dtype")
     x_dtype = DTYPE_BF16 if x.dtype == torch.bfloat16 else DTYPE_F32
-    ws_need = workspace_size(M, 0, K, x_dtype)
+    # f32 x: the x planes (required); bf16 x: the largest member's optional split-K space
+    ws_need = max(workspace_size(M, lin.out_features, K, x_dtype) for lin in lins)
     ws_ptr, ws_bytes = None, 0
-    if ws_need:
-        if workspace is None:
-            workspace = torch.empty(ws_need, dtype=torch.uint8, device=x.device)
+    if workspace is None and ws_need:
+        workspace = torch.empty(ws_need, dtype=torch.uint8, device=x.device)
+    if workspace is not None and workspace.numel():
         ws_ptr, ws_bytes = workspace.data_ptr(), workspace.numel() * workspace.element_size()
     n = len(lins)
     arr = lambda vals: (ctypes.c_void_p * n)(*vals)

@@ -137,7 +137,10 @@ int w4a16_linear(const void *x, int32_t x_dtype,
  * exactly what w4a16_linear gives for that weight; at decode (M <= 4) the n
  * linears run as one launch, otherwise one launch each.  pk, sc, y and N are
  * host arrays of n entries; every weight has K columns and the same group.
- * Workspace as w4a16_linear (w4a16_workspace_size(M, 0, K, x_dtype)).
+ * Workspace as w4a16_linear: f32 x needs w4a16_workspace_size(M, 0, K, x_dtype);
+ * with bf16 x, optional, each member that runs as its own launch takes the
+ * split-K route when ws_bytes reaches w4a16_workspace_size(M, N_j, K, x_dtype)
+ * (pass the largest over the members for all of them).
  */
 int w4a16_linear_group(const void *x, int32_t x_dtype, int32_t n,
                        const int32_t *const *pk, const uint16_t *const *sc,

@@ -612,6 +612,8 @@ def test_prefill_kernel_small_m(M, N, K, monkeypatch):
     (20, (40, 24, 16), 256, False, "bf16"),         # above M = 16: one launch per weight
     (8, (4096, 2048, 2048), 3840, False, "f32"),     # batched decode M = 8: one launch (16-row GEMV)
     (13, (17, 0, 33, 5), 512, False, "f32"),        # M = 13, ragged N, an empty member
+    (32, (4096, 2048, 2048), 3840, False, "bf16"),  # M = 32: each member split-K (skinny form)
+    (128, (4096, 2048, 0), 3840, False, "f32"),     # M = 128: each member split-K (LDS prefill form)
 ])
 def test_linear_group_equals_single_linears(M, Ns, K, x_f32, out):
     """w4a16_linear_group (q, k, v read the same x, engine.zig:552,571,583): every output

@@ -249,14 +249,15 @@ def test_cpp_gate_up_gelu_on_gpu(tool, tmp_path, M, out):
 
 
 @pytest.mark.gpu
-@pytest.mark.parametrize("layer,M", [(0, 1), (5, 3)])
-def test_cpp_qkv_group_on_gpu(tool, tmp_path, layer, M):
+@pytest.mark.parametrize("layer,M,k", [(0, 1, 64), (5, 3, 64), (0, 24, 512)])
+def test_cpp_qkv_group_on_gpu(tool, tmp_path, layer, M, k):
     """linear_group through the C++ mirror on the 12B key layout: q, k and (sliding layer 0)
     v, or q and k only (full layer 5, K = V), each against the oracle's single linear with
-    the bf16-output bound of test_cpp_w4lin_linear_and_dequant_on_gpu."""
+    the bf16-output bound of test_cpp_w4lin_linear_and_dequant_on_gpu.  At M = 24, K = 512
+    the members run one launch each on the split-K route with the tool's workspace."""
     if not torch.cuda.is_available():
         pytest.skip("no GPU")
-    n, k = 32, 64
+    n = 32
     path = str(tmp_path / "g12.safetensors")
     t = g12_like(path, layers=6, n=n, k=k)
     x = o.synth_x(M, k, 21)
@@ -265,6 +266,7 @@ def test_cpp_qkv_group_on_gpu(tool, tmp_path, layer, M):
     assert rc == 0, err
     mods = ["q", "k"] if layer == 5 else ["q", "k", "v"]
     assert json.loads(outp)["linears"] == len(mods)
+    assert (json.loads(outp)["workspace"] > 0) == (M == 24)
     assert not (tmp_path / "y.v.bin").exists() if layer == 5 else True
     gam = k * 2.0 ** -24 / (1 - k * 2.0 ** -24)
     for mname in mods:
