@@ -1617,7 +1617,8 @@ hipError_t w4l_fill_zero(void* p, int64_t bytes, hipStream_t st) {
 
 
 bool w4l_gemv16_plan(int64_t M, int64_t N, int64_t K, int nterms, int* nst_out, int* waves_out, int* xpt_out);
-// 4 < M <= 16 through the GEMV when its plan holds and every 16-row tile
+// M <= 16 through the 16-row GEMV (for M <= 4 where the 4-row plan does not
+// hold) when its plan holds and every 16-row tile
 // re-reading x from L2 stays under 40 MiB (W4A16_GEMV16_XBYTES overrides):
 // measured on the 12B and E2B rows, the GEMV wins 1.2-1.9x below that (q, k/v, o,
 // E2B) and the skinny kernel, whose workgroups share x over 64-128 rows, wins
@@ -1684,7 +1685,7 @@ bool w4l_gemv_fast_plan(int64_t M, int64_t N, int64_t K, int nterms, int* nst_ou
 // at most 8 x vectors; x [M][K] sits in LDS whole (up to 160 KB on gfx950).
 // W4A16_GEMV16=0 turns the route off (tuning).
 bool w4l_gemv16_plan(int64_t M, int64_t N, int64_t K, int nterms, int* nst_out, int* waves_out, int* xpt_out) {
-  if (nterms != 1 || M <= 4 || M > 16 || K % w4k::GSTEP != 0 || N <= 0) return false;
+  if (nterms != 1 || M < 1 || M > 16 || K % w4k::GSTEP != 0 || N <= 0) return false;
   if (const char* e = getenv("W4A16_GEMV16"))
     if (atoi(e) == 0) return false;
   const int64_t steps = K / w4k::GSTEP;
@@ -1833,7 +1834,15 @@ hipError_t w4l_gemv(const uint16_t* x_planes, int nterms, const int32_t* pk, con
                     void* y, int y_f32, int64_t M, int64_t N, int64_t K, int32_t group,
                     hipStream_t st, const W4Pair* pair) {
   if (pair) N = 16 * ((pair->F + 7) / 8);
-  if (M > 4) {
+  bool m16 = M > 4;
+  if (!m16 && nterms == 1) {
+    // M <= 4 beyond the 4-row form (x over its 64 KiB of LDS or 8 vectors per
+    // thread): the 16-row form
+    int a0, a1, a2, a3;
+    const bool four = w4l_gemv_ok(M, K, 1) && w4l_gemv_fast_plan(M, N, K, 1, &a0, &a1, &a2, &a3);
+    m16 = !four && w4l_gemv16_plan(M, N, K, 1, &a0, &a1, &a2);
+  }
+  if (m16) {
     int nst, waves, xpt;
     if (!w4l_gemv16_plan(M, N, K, nterms, &nst, &waves, &xpt)) return hipErrorInvalidValue;
     w4k::GemvArgs a{};
@@ -2319,8 +2328,16 @@ hipError_t w4l_splitk(const uint16_t* x, const int32_t* pk, const uint16_t* sc, 
 hipError_t w4l_linear(const uint16_t* x_planes, int nterms, const int32_t* pk, const uint16_t* sc,
                       void* y, int y_f32, int64_t M, int64_t N, int64_t K, int32_t group,
                       hipStream_t st) {
-  if (w4l_gemv_ok(M, K, nterms)) return w4l_gemv(x_planes, nterms, pk, sc, y, y_f32, M, N, K, group, st);
+  {
+    int a0, a1, a2, a3;
+    if (w4l_gemv_ok(M, K, nterms) && w4l_gemv_fast_plan(M, N, K, nterms, &a0, &a1, &a2, &a3))
+      return w4l_gemv(x_planes, nterms, pk, sc, y, y_f32, M, N, K, group, st);
+  }
   if (w4l_gemv16_ok(M, N, K, nterms)) return w4l_gemv(x_planes, nterms, pk, sc, y, y_f32, M, N, K, group, st);
+  // M <= 4 beyond both GEMV plans (12B gate/up rows at M = 4): the skinny kernel,
+  // 23.5 -> 19 us against the generic GEMV below
+  if (M <= 4 && nterms == 1 && K % 256 == 0) return w4l_skinny(x_planes, pk, sc, y, y_f32, M, N, K, group, st);
+  if (w4l_gemv_ok(M, K, nterms)) return w4l_gemv(x_planes, nterms, pk, sc, y, y_f32, M, N, K, group, st);
   if (w4l_prefill_ok(M, K, nterms)) return w4l_prefill(x_planes, pk, sc, y, y_f32, M, N, K, group, st);
   // W4A16_PF_SMALL=1: tuning switch, 4 < M <= 64 through the 32x32 kernel
   if (getenv("W4A16_PF_SMALL") && nterms == 1 && M > 4 && K % 64 == 0)
@@ -2406,15 +2423,17 @@ hipError_t w4l_gelu_mul(const float* g, const float* u, void* h, int h_f32, int 
 
 bool w4l_group_fused(int64_t M, int64_t Ntot, int64_t K, int nterms) {
   int nst, waves, xpt, tpw;
-  if (M > 4) return w4l_gemv16_ok(M, Ntot, K, nterms);
-  return w4l_gemv_ok(M, K, nterms) && w4l_gemv_fast_plan(M, 16, K, nterms, &nst, &waves, &xpt, &tpw);
+  if (M <= 4 && w4l_gemv_ok(M, K, nterms) && w4l_gemv_fast_plan(M, 16, K, nterms, &nst, &waves, &xpt, &tpw))
+    return true;
+  return w4l_gemv16_ok(M, Ntot, K, nterms);
 }
 
 hipError_t w4l_gemv_group(const uint16_t* x_planes, int nterms, int n, const int32_t* const* pk,
                           const uint16_t* const* sc, void* const* y, const int64_t* N, int y_f32, int64_t M, int64_t K,
                           int32_t group, hipStream_t st) {
   int nst, waves, xpt, tpw;
-  const bool m16 = M > 4;
+  // the 4-row form where its plan holds, else the 16-row form (M <= 16)
+  const bool m16 = M > 4 || !w4l_gemv_ok(M, K, nterms) || !w4l_gemv_fast_plan(M, 16, K, nterms, &nst, &waves, &xpt, &tpw);
   if (n < 1 || n > 4) return hipErrorInvalidValue;
   if (m16 ? !w4l_gemv16_plan(M, 16, K, nterms, &nst, &waves, &xpt)
           : (!w4l_gemv_ok(M, K, nterms) || !w4l_gemv_fast_plan(M, 16, K, nterms, &nst, &waves, &xpt, &tpw)))

@@ -115,7 +115,8 @@ CASES = [
     (3, 33, 512, 64, False, True, True),        # GEMV, group 64, bf16 dots
     (1, 72, 1024, 32, True, True, False),       # GEMV on f32 x (three bf16 planes)
     (1, 15360, 3840, 32, False, True, False),   # 12B gate/up decode
-    (4, 70, 3840, 32, False, True, False),      # M = 4 at K = 3840 -> skinny
+    (4, 70, 3840, 32, False, True, False),      # M = 4 at K = 3840: beyond the 4-row plan -> 16-row GEMV
+    (4, 15360, 3840, 32, False, False, False),  # 12B gate/up at M = 4: beyond both GEMV plans -> skinny
     (5, 33, 256, 32, False, False, False),      # 16-row GEMV pair mode
     (8, 6144, 1536, 32, False, True, False),    # 16-row GEMV pair mode: E2B gate/up at M = 8
     (16, 72, 1024, 64, False, False, True),     # 16-row GEMV pair mode, group 64, bf16 dots, h bf16

@@ -289,18 +289,26 @@ def test_linear_c4_12b_gateup(M):
 
 @pytest.mark.parametrize("M,K,N", [
     (5, 3840, 4096), (8, 4096, 3840), (13, 1536, 2048), (16, 3840, 2048), (16, 2048, 1536), (12, 256, 40),
+    (4, 3840, 4096),    # M = 4 beyond the 4-row plan (x over 8 vectors per thread)
+    (3, 15360, 1000),   # M = 3 with x over the 4-row form's 64 KiB of LDS
 ])
 def test_linear_gemv16_route(M, K, N):
-    """4 < M <= 16 on the smaller rows: the straight-line GEMV with its 16-row epilogue
-    (x whole in LDS, up to 160 KB) against the oracle, f32 and bf16 outputs."""
+    """M <= 16 on the smaller rows (M <= 4 where the 4-row plan does not hold): the
+    straight-line GEMV with its 16-row epilogue (x whole in LDS, up to 160 KB), one
+    pass (empty workspace), against the oracle, f32 and bf16 outputs."""
     say(f"gemv16 M={M} K={K} N={N}")
     _, pk, sc = o.synth_weights(N, K, 1300 + N)
     x = o.synth_x(M, K, 1400 + M)
     w = o.dequant(pk, sc)
     ref32 = o.matmul_f32(x, w)
-    check_f32(gpu_linear(x, pk, sc, "f32"), x, w, K, ref32)
+    none = torch.empty(0, dtype=torch.uint8, device="cuda")
+    xt, pkt, sct = dev_u16(x), dev(pk), dev_u16(sc)
+    y = w4a16.linear(xt, pkt, sct, out_dtype=torch.float32, workspace=none)
+    yb = w4a16.linear(xt, pkt, sct, out_dtype=torch.bfloat16, workspace=none)
+    torch.cuda.synchronize()
+    check_f32(y.cpu().numpy(), x, w, K, ref32)
     _, mag = o.matmul_f64(x, w)
-    check_bf16(gpu_linear(x, pk, sc, "bf16"), ref32, mag, K)
+    check_bf16(host_u16(yb), ref32, mag, K)
 
 
 @pytest.mark.parametrize("M,K,N,step", [
@@ -603,6 +611,22 @@ def test_prefill_kernel_small_m(M, N, K, monkeypatch):
     yb = gpu_linear(x, pk, sc, "bf16")
     _, mag = o.matmul_f64(x, w)
     check_bf16(yb, ref32, mag, K)
+
+
+def test_linear_m4_beyond_both_gemv_plans():
+    """12B gate/up rows at M = 4 (x re-read per 16-row tile over the 16-row GEMV's
+    limit): the skinny kernel, x rows past M repeating row M - 1; every 11th row n
+    against the oracle, f32 and bf16 outputs."""
+    M, K, N = 4, 3840, 30720
+    say(f"M=4 beyond both GEMV plans K={K} N={N}")
+    _, pk, sc = o.synth_weights(N, K, 1700)
+    x = o.synth_x(M, K, 1701)
+    rows = np.arange(0, N, 11)
+    w = o.dequant(pk[rows], sc[rows])
+    ref32 = o.matmul_f32(x, w)
+    check_f32(gpu_linear(x, pk, sc, "f32")[:, rows], x, w, K, ref32)
+    _, mag = o.matmul_f64(x, w)
+    check_bf16(gpu_linear(x, pk, sc, "bf16")[:, rows], ref32, mag, K)
 
 
 @pytest.mark.parametrize("M,Ns,K,x_f32,out", [
