@@ -2175,7 +2175,7 @@ hipError_t w4l_prefill(const uint16_t* x, const int32_t* pk, const uint16_t* sc,
 //    32 / 64 23.2 / 23.7 / 23.8 / 27.5 -> 15.5 / 15.9 / 18.5 / 25.3; q, o, k/v at
 //    M = 32 15.4, 12.6, 12.7 -> 10.2, 10.3, 9.6 and at M = 64 20.2, 21.6, 17.3 ->
 //    13.4, 13.3, 11.4 (each against the prefill form).
-//  - prefill (otherwise, M > 4): workgroups of WS waves x 32 W rows (256 rows for
+//  - prefill (K % 256 != 0, M > 4): workgroups of WS waves x 32 W rows (256 rows for
 //    M > 32, 128 for M <= 32; x blocks of 64 / 32 rows) and kq parts, the
 //    smallest divisor of K / 64 (<= 16) that gives >= 240 workgroups, else the
 //    largest.
@@ -2239,6 +2239,10 @@ bool splitk_plan(int64_t M, int64_t N, int64_t K, int nterms, SplitPlan* p) {
       *p = SplitPlan{SPLIT_SKINNY, q, 0, 0};
       return true;
     }
+    // no part count within 256 workgroups: the one-pass grid already has > 128,
+    // and the 32x32 form below is slower there (E2B gate/up rows at M = 17 / 32 /
+    // 64: 14.2 / 15.6 / 24.4 us against 8.0 / 8.4 / 11.8 one-pass)
+    return false;
   }
   const int mb = M <= 32 ? 1 : 2;
   const int ws = mb == 2 ? 8 : 4;

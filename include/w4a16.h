@@ -93,7 +93,9 @@ int w4a16_dequant(const int32_t *pk, const uint16_t *sc, uint16_t *w,
  * workgroups of 256 x 128, and N <= 8192 up to M = 128; or N < 16384 and:
  * 16 < M <= 64; 4 < M <= 16 beyond the 16-row decode GEMV with K >= 8192 or
  * N < 8192; M <= 4 with K % 256 == 0 and x beyond the decode GEMV's 64 KiB of
- * LDS -- the 12B q/k/v/o rows at M > 16, down at M >= 3 up to M = 1024, E2B
+ * LDS; with K % 256 == 0 at M <= 64 only while the skinny kernel's one-pass grid
+ * has at most 128 workgroups -- the 12B q/k/v/o rows at M > 16, down at M >= 3 up
+ * to M = 1024, E2B
  * down at M = 16) it is the size of kq f32 partial planes, kq * M * N * 4 bytes
  * rounded up to 256 with 2 <= kq <= 64 K parts; given at least that much, the
  * call splits K across workgroups and adds the parts in a second launch in a

@@ -128,7 +128,7 @@ def splitk_bytes(M, N, K):
     16-row GEMV with K >= 8192 or N < 8192; or M <= 4 outside the decode GEMV
     with K % 256 == 0.  Skinny form (K % 256 == 0): kq = the largest divisor
     q <= 64 of K / 256 with ceil(N / 64) * (x blocks of 16, 32 or 64 rows) * q
-    <= 256.  Otherwise (M > 4) the 32x32 form: the smallest divisor q <= 16 of
+    <= 256 (none: no split).  K % 256 != 0 (M > 4): the 32x32 form, the smallest divisor q <= 16 of
     K / 64 with tiles * q >= 240 (tiles of 256 W rows at M > 32, 128 below),
     else the largest."""
     if M > 64 and N > 0 and K % 64 == 0:
@@ -151,7 +151,9 @@ def splitk_bytes(M, N, K):
         mt = 1 if M <= 16 else 2 if M <= 32 else 4
         per_part = -(-N // 64) * -(-M // (16 * mt))
         fits = [c for c in range(2, min(nk, 64) + 1) if nk % c == 0 and per_part * c <= 256]
-        q = fits[-1] if fits else 0
+        if not fits:
+            return 0  # the one-pass grid already has > 128 workgroups
+        q = fits[-1]
     if not q:
         if M <= 4:
             return 0
@@ -177,7 +179,7 @@ def test_workspace_size(L):
     (8, 3840, 15360, 4 * 8 * 3840 * 4),     # M = 8 at K >= 8192: 60 x 4
     (64, 4096, 3840, 3 * 64 * 4096 * 4),    # 12B q: 64 blocks, 3 | 15 chunks
     (64, 2048, 3840, 5 * 64 * 2048 * 4),    # k/v: 32 blocks x 5
-    (32, 12288, 1536, 3 * 32 * 12288 * 4),  # E2B gate/up rows at M = 32: 192 blocks, 32x32 form
+    (32, 12288, 1536, 0),                   # E2B gate/up rows at M = 32: 192 blocks one-pass, no skinny part count
     (16, 1536, 6144, 8 * 16 * 1536 * 4),    # E2B down at M = 16: beyond the 16-row GEMV, 24 x 8
     (4, 3840, 15360, 4 * 4 * 3840 * 4),     # M = 4: x beyond the decode GEMV's LDS
     (24, 700, 1152, 604928),                # K % 256 != 0: 32x32 form, 9 parts (9 * 24 * 700 * 4 rounded up to 256)

@@ -124,7 +124,7 @@ CASES = [
     (40, 129, 1280, 32, False, True, True),     # split-K (skinny form, 5 parts), bf16 dots
     (64, 200, 768, 128, False, True, False),    # split-K (skinny form, 400 virtual rows), group 128
     (16, 1000, 6144, 32, False, False, False),  # split-K at M = 16 beyond the 16-row GEMV (8 parts), h bf16
-    (32, 6144, 1536, 32, False, True, False),   # split-K (prefill form): E2B gate/up at M = 32
+    (32, 6144, 1536, 32, False, True, False),   # E2B gate/up at M = 32: one-pass skinny (no split part count)
     (65, 50, 64, 32, False, True, False),       # prefill
     (300, 130, 192, 64, False, False, False),   # prefill, h bf16
     (257, 17, 320, 32, False, True, True),      # prefill, bf16 dots
@@ -161,9 +161,10 @@ def test_gate_up_gelu_12b_skinny_eight_waves(M):
 
 @pytest.mark.parametrize("h_f32", [True, False])
 def test_gate_up_gelu_one_pass_without_workspace(h_f32):
-    """E2B gate/up at M = 48: with an empty workspace the call takes the one-pass
-    skinny route instead of split-K; both meet the bound."""
-    M, F, K = 48, 6144, 1536
+    """Gate/up at M = 48, F = 1000, K = 1536 (split-K, skinny form, 6 parts by default):
+    with an empty workspace the call takes the one-pass skinny route instead; both
+    meet the bound."""
+    M, F, K = 48, 1000, 1536
     say(f"gate_up_gelu one-pass M={M} F={F} K={K} h_f32={h_f32}")
     assert w4a16.gate_up_workspace_size(M, F, K, w4a16.DTYPE_BF16) > 0
     pk_g, sc_g, pk_u, sc_u = weights(F, K, 4600, 32)
