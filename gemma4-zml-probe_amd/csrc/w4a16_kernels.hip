@@ -2158,8 +2158,9 @@ hipError_t w4l_prefill(const uint16_t* x, const int32_t* pk, const uint16_t* sc,
   return hipGetLastError();
 }
 
-// Split-K plan (bf16 x, M <= 64, N < 16384) for the shapes whose one-pass grid
-// cannot fill the GPU:
+// Split-K plan (bf16 x) for the shapes whose one-pass grid cannot fill the GPU.
+// Above M = 64: the skinny form up to M = 128 when K % 256 == 0 (else one pass),
+// the LDS prefill form beyond (comments in the branch).  Up to M = 64, N < 16384:
 //  - M <= 4 when x is too large for the decode GEMV's LDS (12B down at M = 3..4:
 //    21.3 -> 15.5 us), skinny form only;
 //  - 4 < M <= 16 when the 16-row GEMV does not take the shape (it is faster
@@ -2192,13 +2193,31 @@ struct SplitPlan {
 bool splitk_plan(int64_t M, int64_t N, int64_t K, int nterms, SplitPlan* p) {
   if (nterms != 1 || M < 1 || K % 64 != 0 || N <= 0) return false;
   if (M > 64) {
-    // prefill_lds_kernel with 256 x 128 tiles over kq K parts when its one-pass
-    // grid is under 240 workgroups (N <= 8192 at M <= 128): the largest divisor of
-    // K / 64 (<= 16) that keeps the grid within 256 workgroups, one per CU (its LDS
-    // holds one workgroup per CU: q at M = 128 took 24.6 us with 192 workgroups
-    // against 31.9 with 320)
+    // 64 < M <= 128: the skinny kernel in two 64-row x blocks over K parts (one
+    // workgroup per CU at most), else one pass; faster than the LDS form on every
+    // row measured (M = 65: 12B down 42.4 -> 40.7 us, E2B down 27.2 -> 20.9,
+    // K = 3840 / N = 1024: 14.7 -> 10.3; where no part count fits, the one-pass
+    // skinny kernel: N = 8192, 28.7 -> 21.3)
+    bool sk = M <= 128 && K % 256 == 0;
+    if (const char* e = getenv("W4A16_SPLITK_SKINNY"))
+      if (atoi(e) == 0) sk = false;
     if (const char* e = getenv("W4A16_SPLITK"))
       if (atoi(e) == 0) return false;
+    if (sk) {
+      const int64_t nk = K / 256;
+      const int64_t per_part = ((N + 63) / 64) * ((M + 63) / 64);
+      int q = 0;
+      for (int c = 2; c <= nk && c <= 64; ++c)
+        if (nk % c == 0 && per_part * c <= 256) q = c;
+      if (q < 2) return false;
+      *p = SplitPlan{SPLIT_SKINNY, q, 0, 0};
+      return true;
+    }
+    // M > 128, or K % 256 != 0: prefill_lds_kernel with 256 x 128 tiles over kq K
+    // parts when its one-pass grid is under 240 workgroups (N <= 8192 at M <= 128):
+    // the largest divisor of K / 64 (<= 16) that keeps the grid within 256
+    // workgroups, one per CU (its LDS holds one workgroup per CU: q at M = 128 took
+    // 24.6 us with 192 workgroups against 31.9 with 320)
     const int64_t grid = ((N + 127) / 128) * ((M + 255) / 256);
     if (grid >= 240) return false;
     // up to 128 rows the one-pass kernel's 128-row x tiles waste no MFMAs, and with
@@ -2329,6 +2348,17 @@ hipError_t w4l_splitk(const uint16_t* x, const int32_t* pk, const uint16_t* sc, 
   return splitk_finalize_launch(part, kq, M, Nv, y, y_f32, pair, st);
 }
 
+// 64 < M <= 128 where the prefill kernel's 128-wide tiles give fewer than 240
+// workgroups: the skinny kernel in two 64-row x blocks (the second reads W from
+// the MALL), 2.2-2.4x faster one-pass (12B down at M = 65: 168 -> 71 us, q:
+// 47 -> 21, E2B gate/up: 21 -> 16).  The 12B gate/up pair (240 tiles) stays on
+// the prefill kernel (48 against 55 us).  W4A16_SKINNY_MID=0 turns it off.
+static bool skinny_mid(int64_t M, int64_t N, int64_t K, int nterms) {
+  if (const char* e = getenv("W4A16_SKINNY_MID"))
+    if (atoi(e) == 0) return false;
+  return M > 64 && M <= 128 && (N + 127) / 128 < 240 && w4l_skinny_ok(M, K, nterms);
+}
+
 hipError_t w4l_linear(const uint16_t* x_planes, int nterms, const int32_t* pk, const uint16_t* sc,
                       void* y, int y_f32, int64_t M, int64_t N, int64_t K, int32_t group,
                       hipStream_t st) {
@@ -2342,6 +2372,7 @@ hipError_t w4l_linear(const uint16_t* x_planes, int nterms, const int32_t* pk, c
   // 23.5 -> 19 us against the generic GEMV below
   if (M <= 4 && nterms == 1 && K % 256 == 0) return w4l_skinny(x_planes, pk, sc, y, y_f32, M, N, K, group, st);
   if (w4l_gemv_ok(M, K, nterms)) return w4l_gemv(x_planes, nterms, pk, sc, y, y_f32, M, N, K, group, st);
+  if (skinny_mid(M, N, K, nterms)) return w4l_skinny(x_planes, pk, sc, y, y_f32, M, N, K, group, st);
   if (w4l_prefill_ok(M, K, nterms)) return w4l_prefill(x_planes, pk, sc, y, y_f32, M, N, K, group, st);
   // W4A16_PF_SMALL=1: tuning switch, 4 < M <= 64 through the 32x32 kernel
   if (getenv("W4A16_PF_SMALL") && nterms == 1 && M > 4 && K % 64 == 0)
@@ -2395,6 +2426,7 @@ PairRoute pair_route(int64_t M, int64_t F, int64_t K, int nterms) {
   if (w4l_gemv_ok(M, K, nterms) && w4l_gemv_fast_plan(M, 16 * ((F + 7) / 8), K, nterms, &nst, &waves, &xpt, &tpw))
     return PAIR_GEMV;
   if (w4l_gemv16_ok(M, 16 * ((F + 7) / 8), K, nterms)) return PAIR_GEMV;
+  if (skinny_mid(M, 16 * ((F + 7) / 8), K, nterms)) return PAIR_SKINNY;
   if (w4l_prefill_ok(M, K, nterms)) return PAIR_PREFILL;
   if (getenv("W4A16_PF_SMALL") && nterms == 1 && M > 4 && K % 64 == 0) return PAIR_PREFILL;
   if (nterms == 1 && K % 256 == 0) return PAIR_SKINNY;

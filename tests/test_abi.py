@@ -120,8 +120,10 @@ def gemv16_ok(M, N, K):
 
 
 def splitk_bytes(M, N, K):
-    """Optional split-K workspace of a bf16 linear (kq f32 partial planes).  Above
-    M = 64: when the LDS prefill kernel's grid (256 x 128 tiles) is under 240
+    """Optional split-K workspace of a bf16 linear (kq f32 partial planes).  At
+    64 < M <= 128 with K % 256 == 0: the skinny form over two 64-row x blocks,
+    kq = the largest divisor q <= 64 of K / 256 with 2 * ceil(N / 64) * q <= 256
+    (none: no split).  Otherwise above M = 64: when the LDS prefill kernel's grid (256 x 128 tiles) is under 240
     workgroups (and N <= 8192 up to M = 128), kq = the largest divisor q <= 16 of
     K / 64 with grid * q <= 256; else
     the largest.  Else taken when N < 16384, K % 64 == 0 and: 16 < M <= 64; or 4 < M <= 16 outside the
@@ -131,6 +133,11 @@ def splitk_bytes(M, N, K):
     <= 256 (none: no split).  K % 256 != 0 (M > 4): the 32x32 form, the smallest divisor q <= 16 of
     K / 64 with tiles * q >= 240 (tiles of 256 W rows at M > 32, 128 below),
     else the largest."""
+    if 64 < M <= 128 and N > 0 and K % 256 == 0:
+        nk = K // 256
+        per_part = -(-N // 64) * 2
+        fits = [c for c in range(2, min(nk, 64) + 1) if nk % c == 0 and per_part * c <= 256]
+        return -(-(fits[-1] * M * N * 4) // 256) * 256 if fits else 0
     if M > 64 and N > 0 and K % 64 == 0:
         # 256 x 128 tiles of the LDS prefill kernel over K parts when its grid is under 240
         grid = -(-N // 128) * -(-M // 256)
@@ -188,14 +195,16 @@ def test_workspace_size(L):
     (8, 6144, 1536, 0),                     # 16-row GEMV (E2B gate/up rows)
     (16, 8192, 3840, 0),                    # beyond the 16-row GEMV, N >= 8192 at K < 8192: one-pass skinny
     (64, 30720, 3840, 0),                   # the skinny grid fills the GPU
-    (65, 3840, 15360, 8 * 65 * 3840 * 4),   # M > 64: LDS prefill form, 30 W blocks x 8 parts
-    (256, 3840, 15360, 8 * 256 * 3840 * 4), # the same at M = 256
+    (65, 3840, 15360, 2 * 65 * 3840 * 4),   # 64 < M <= 128: skinny form, 60 W blocks x 2 x blocks x 2 parts
+    (96, 1536, 6144, 4 * 96 * 1536 * 4),    # E2B down at M = 96: 24 W blocks x 2 x blocks x 4 parts
+    (100, 1000, 4160, 5200128),             # K % 256 != 0 above M = 64: LDS prefill form, 8 W blocks x 13 parts (rounded up to 256)
+    (256, 3840, 15360, 8 * 256 * 3840 * 4), # M > 128: LDS prefill form, 30 W blocks x 8 parts
     (200, 1000, 4096, 16 * 200 * 1000 * 4), # 8 W blocks x 16 parts
-    (128, 4096, 3840, 6 * 128 * 4096 * 4),  # q at M = 128: 32 W blocks x 6 parts (192 <= 256 workgroups)
+    (128, 4096, 3840, 0),                   # q at M = 128: no part count of K / 256 = 15 fits, one-pass skinny
     (2048, 3840, 15360, 0),                 # 240 workgroups one-pass: no split
     (128, 30720, 3840, 0),                  # 240 W blocks
-    (128, 12288, 1536, 0),                  # M <= 128 with N > 8192: the one-pass 128-row tiles
-    (128, 8192, 3840, 4 * 128 * 8192 * 4),  # full-layer q at M = 128: 64 W blocks x 4 parts
+    (128, 12288, 1536, 0),                  # 384 skinny workgroups one-pass
+    (128, 8192, 3840, 0),                   # full-layer q at M = 128: one-pass skinny (256 workgroups)
     (64, 3840, 15360 + 32, 0),              # K % 64 != 0
 ])
 def test_workspace_size_splitk(L, M, N, K, expect):

@@ -126,6 +126,8 @@ CASES = [
     (16, 1000, 6144, 32, False, False, False),  # split-K at M = 16 beyond the 16-row GEMV (8 parts), h bf16
     (32, 6144, 1536, 32, False, True, False),   # E2B gate/up at M = 32: one-pass skinny (no split part count)
     (65, 50, 64, 32, False, True, False),       # prefill
+    (100, 6144, 1536, 32, False, True, False),  # E2B gate/up at M = 100: one-pass skinny over two 64-row x blocks
+    (96, 40, 512, 64, False, False, True),      # skinny over two x blocks, group 64, bf16 dots, h bf16
     (300, 130, 192, 64, False, False, False),   # prefill, h bf16
     (257, 17, 320, 32, False, True, True),      # prefill, bf16 dots
     (4096, 4096, 64, 32, False, True, False),   # prefill with two W blocks per wave

@@ -321,14 +321,16 @@ def test_linear_gemv16_route(M, K, N):
     (4, 15360, 520, 1),     # M = 4 with x beyond the decode GEMV's LDS: 20 parts, ragged N
     (3, 12288, 256, 1),     # M = 3: 48 parts of one chunk
     (24, 1152, 700, 1),     # prefill form: K % 256 != 0, 9 parts of 128 columns
-    (65, 15360, 3840, 13),  # M > 64: LDS prefill form, 30 W blocks x 8 parts, one real row in the second half
+    (65, 15360, 3840, 13),  # 64 < M <= 128: skinny form, two 64-row x blocks (one real row in the second), 2 parts
+    (128, 6144, 1536, 5),   # E2B down at M = 128: skinny form, 24 W blocks x 2 x blocks x 4 parts
+    (100, 4160, 1000, 1),   # K % 256 != 0 above M = 64: LDS prefill form, 13 parts
     (200, 4096, 1000, 1),   # LDS form, ragged N, 16 parts
     (300, 1152, 700, 3),    # LDS form, two x blocks, K % 256 != 0, 9 parts of 2 steps
 ])
 def test_linear_splitk_route(M, K, N, step):
     """The split-K route (bf16 x, a one-pass grid too small to fill the GPU; the
-    skinny kernel over K parts, the 32x32 kernel when K % 256 != 0, and above
-    M = 64 the LDS prefill kernel): the
+    skinny kernel over K parts, also over two 64-row x blocks up to M = 128, the
+    32x32 kernel when K % 256 != 0, and above M = 64 the LDS prefill kernel): the
     default call (the wrapper allocates the optional workspace) and the one-pass
     route (no workspace) both meet the stated f32 tolerance against the oracle on
     every `step`-th row n; bf16 outputs meet the bf16 bound."""
@@ -510,11 +512,11 @@ def test_graph_capture_replays_match_eager():
         del junk
 
 
-@pytest.mark.parametrize("M,K,N", [(8, 15360, 1000), (24, 1152, 700), (100, 2048, 700)])
+@pytest.mark.parametrize("M,K,N", [(8, 15360, 1000), (24, 1152, 700), (200, 2048, 700), (100, 2048, 700)])
 def test_splitk_graph_replays_match_eager(M, K, N):
     """The split-K route (main kernel + finalize over the caller's workspace; the
-    skinny form with 15 parts, the 32x32 form with 9, the LDS prefill form with 16)
-    captured in a HIP graph:
+    skinny form with 15 parts, the 32x32 form with 9, the LDS prefill form with 16,
+    the skinny form over two 64-row x blocks with 8) captured in a HIP graph:
     every replay equals the eager result bit for bit, since the parts are added
     in a fixed order, with other eager work between the replays."""
     say(f"split-K graph capture / replay M={M} K={K} N={N}")
