@@ -2158,9 +2158,17 @@ hipError_t w4l_prefill(const uint16_t* x, const int32_t* pk, const uint16_t* sc,
   return hipGetLastError();
 }
 
+// Upper bound of the rows above 64 that the skinny kernel takes in several
+// 64-row x blocks (W4A16_SKINNY_MID=<M>, tuning; 0 turns it off).
+static int64_t skinny_mid_max() {
+  if (const char* e = getenv("W4A16_SKINNY_MID")) return atoll(e);
+  return 256;
+}
+
 // Split-K plan (bf16 x) for the shapes whose one-pass grid cannot fill the GPU.
-// Above M = 64: the skinny form up to M = 128 when K % 256 == 0 (else one pass),
-// the LDS prefill form beyond (comments in the branch).  Up to M = 64, N < 16384:
+// Above M = 64: the skinny form up to M = 128 when K % 256 == 0, and up to 256
+// when also K <= 8192 (else one pass); the LDS prefill form beyond (comments in
+// the branch).  Up to M = 64, N < 16384:
 //  - M <= 4 when x is too large for the decode GEMV's LDS (12B down at M = 3..4:
 //    21.3 -> 15.5 us), skinny form only;
 //  - 4 < M <= 16 when the 16-row GEMV does not take the shape (it is faster
@@ -2198,7 +2206,11 @@ bool splitk_plan(int64_t M, int64_t N, int64_t K, int nterms, SplitPlan* p) {
     // row measured (M = 65: 12B down 42.4 -> 40.7 us, E2B down 27.2 -> 20.9,
     // K = 3840 / N = 1024: 14.7 -> 10.3; where no part count fits, the one-pass
     // skinny kernel: N = 8192, 28.7 -> 21.3)
-    bool sk = M <= 128 && K % 256 == 0;
+    // 128 < M <= 256 (three or four x blocks) only for K <= 8192: 3840 -> 1024 /
+    // 4096 at M = 160 17.8 / 26.1 -> 11.2 / 21.4 us, E2B down 23.7 -> 17.0, but
+    // 12B down 48.8 against 72.5 and the E2B model projection (K = 15360) 30.8
+    // against 41.6 at M = 256, where the LDS form splits K into more parts
+    bool sk = K % 256 == 0 && M <= skinny_mid_max() && (M <= 128 || K <= 8192);
     if (const char* e = getenv("W4A16_SPLITK_SKINNY"))
       if (atoi(e) == 0) sk = false;
     if (const char* e = getenv("W4A16_SPLITK"))
@@ -2213,7 +2225,7 @@ bool splitk_plan(int64_t M, int64_t N, int64_t K, int nterms, SplitPlan* p) {
       *p = SplitPlan{SPLIT_SKINNY, q, 0, 0};
       return true;
     }
-    // M > 128, or K % 256 != 0: prefill_lds_kernel with 256 x 128 tiles over kq K
+    // the other rows: prefill_lds_kernel with 256 x 128 tiles over kq K
     // parts when its one-pass grid is under 240 workgroups (N <= 8192 at M <= 128):
     // the largest divisor of K / 64 (<= 16) that keeps the grid within 256
     // workgroups, one per CU (its LDS holds one workgroup per CU: q at M = 128 took
@@ -2348,15 +2360,15 @@ hipError_t w4l_splitk(const uint16_t* x, const int32_t* pk, const uint16_t* sc, 
   return splitk_finalize_launch(part, kq, M, Nv, y, y_f32, pair, st);
 }
 
-// 64 < M <= 128 where the prefill kernel's 128-wide tiles give fewer than 240
-// workgroups: the skinny kernel in two 64-row x blocks (the second reads W from
-// the MALL), 2.2-2.4x faster one-pass (12B down at M = 65: 168 -> 71 us, q:
-// 47 -> 21, E2B gate/up: 21 -> 16).  The 12B gate/up pair (240 tiles) stays on
-// the prefill kernel (48 against 55 us).  W4A16_SKINNY_MID=0 turns it off.
+// 64 < M <= 256 where the prefill kernel's 128-wide tiles give fewer than 240
+// workgroups: the skinny kernel in two to four 64-row x blocks (the later ones
+// read W mostly from the MALL), 2.2-2.4x faster one-pass up to M = 128 (12B down
+// at M = 65: 168 -> 71 us, q: 47 -> 21, E2B gate/up: 21 -> 16) and ahead of the
+// LDS kernel's 256-row tiles above (E2B gate/up at M = 160 / 256: 30.4 / 32.6 ->
+// 26.0 / 27.3).  The 12B gate/up pair (240 tiles) stays on the prefill kernels
+// (48 against 55 us at M = 65, a tie at 160-256).
 static bool skinny_mid(int64_t M, int64_t N, int64_t K, int nterms) {
-  if (const char* e = getenv("W4A16_SKINNY_MID"))
-    if (atoi(e) == 0) return false;
-  return M > 64 && M <= 128 && (N + 127) / 128 < 240 && w4l_skinny_ok(M, K, nterms);
+  return M > 64 && M <= skinny_mid_max() && (N + 127) / 128 < 240 && w4l_skinny_ok(M, K, nterms);
 }
 
 hipError_t w4l_linear(const uint16_t* x_planes, int nterms, const int32_t* pk, const uint16_t* sc,

@@ -89,10 +89,11 @@ int w4a16_dequant(const int32_t *pk, const uint16_t *sc, uint16_t *w,
  * x_dtype = W4A16_DTYPE_F32: 6 * M * K bytes (rounded up to 256) to hold the
  * three bf16 terms of x, required.
  * x_dtype = W4A16_DTYPE_BF16: nothing is required.  On shapes whose one-pass
- * kernel cannot fill the GPU (K % 64 == 0, and: 64 < M <= 128 with K % 256 == 0
- * while the skinny kernel's grid of 2 * ceil(N / 64) workgroups is at most 128
- * (N <= 4096); M > 128, or K % 256 != 0 above M = 64, with fewer than 240
- * workgroups of 256 x 128, and N <= 8192 up to M = 128; or N < 16384 and:
+ * kernel cannot fill the GPU (K % 64 == 0, and: 64 < M <= 128, or up to 256
+ * with K <= 8192, with K % 256 == 0 while the skinny kernel's grid of
+ * ceil(M / 64) * ceil(N / 64) workgroups is at most 128; other rows above
+ * M = 64 with fewer than 240 workgroups of 256 x 128, and N <= 8192 up to
+ * M = 128; or N < 16384 and:
  * 16 < M <= 64; 4 < M <= 16 beyond the 16-row decode GEMV with K >= 8192 or
  * N < 8192; M <= 4 with K % 256 == 0 and x beyond the decode GEMV's 64 KiB of
  * LDS; with K % 256 == 0 at M <= 64 only while the skinny kernel's one-pass grid

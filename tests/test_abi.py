@@ -121,9 +121,9 @@ def gemv16_ok(M, N, K):
 
 def splitk_bytes(M, N, K):
     """Optional split-K workspace of a bf16 linear (kq f32 partial planes).  At
-    64 < M <= 128 with K % 256 == 0: the skinny form over two 64-row x blocks,
-    kq = the largest divisor q <= 64 of K / 256 with 2 * ceil(N / 64) * q <= 256
-    (none: no split).  Otherwise above M = 64: when the LDS prefill kernel's grid (256 x 128 tiles) is under 240
+    64 < M <= 128, or up to 256 with K <= 8192, with K % 256 == 0: the skinny form
+    over 64-row x blocks, kq = the largest divisor q <= 64 of K / 256 with
+    ceil(M / 64) * ceil(N / 64) * q <= 256 (none: no split).  Otherwise above M = 64: when the LDS prefill kernel's grid (256 x 128 tiles) is under 240
     workgroups (and N <= 8192 up to M = 128), kq = the largest divisor q <= 16 of
     K / 64 with grid * q <= 256; else
     the largest.  Else taken when N < 16384, K % 64 == 0 and: 16 < M <= 64; or 4 < M <= 16 outside the
@@ -133,9 +133,9 @@ def splitk_bytes(M, N, K):
     <= 256 (none: no split).  K % 256 != 0 (M > 4): the 32x32 form, the smallest divisor q <= 16 of
     K / 64 with tiles * q >= 240 (tiles of 256 W rows at M > 32, 128 below),
     else the largest."""
-    if 64 < M <= 128 and N > 0 and K % 256 == 0:
+    if 64 < M <= 256 and N > 0 and K % 256 == 0 and (M <= 128 or K <= 8192):
         nk = K // 256
-        per_part = -(-N // 64) * 2
+        per_part = -(-N // 64) * -(-M // 64)
         fits = [c for c in range(2, min(nk, 64) + 1) if nk % c == 0 and per_part * c <= 256]
         return -(-(fits[-1] * M * N * 4) // 256) * 256 if fits else 0
     if M > 64 and N > 0 and K % 64 == 0:
@@ -199,7 +199,10 @@ def test_workspace_size(L):
     (96, 1536, 6144, 4 * 96 * 1536 * 4),    # E2B down at M = 96: 24 W blocks x 2 x blocks x 4 parts
     (100, 1000, 4160, 5200128),             # K % 256 != 0 above M = 64: LDS prefill form, 8 W blocks x 13 parts (rounded up to 256)
     (256, 3840, 15360, 8 * 256 * 3840 * 4), # M > 128: LDS prefill form, 30 W blocks x 8 parts
-    (200, 1000, 4096, 16 * 200 * 1000 * 4), # 8 W blocks x 16 parts
+    (200, 1000, 4096, 4 * 200 * 1000 * 4),  # skinny form, 16 W blocks x 4 x blocks x 4 parts
+    (300, 1000, 4096, 16 * 300 * 1000 * 4), # M > 256: LDS prefill form, 8 W blocks x 2 x blocks x 16 parts
+    (256, 1536, 6144, 2 * 256 * 1536 * 4),  # E2B down at M = 256: skinny form, 24 x 4 x 2 parts
+    (160, 4096, 3840, 0),                   # no part count fits 192 skinny workgroups: one-pass skinny
     (128, 4096, 3840, 0),                   # q at M = 128: no part count of K / 256 = 15 fits, one-pass skinny
     (2048, 3840, 15360, 0),                 # 240 workgroups one-pass: no split
     (128, 30720, 3840, 0),                  # 240 W blocks

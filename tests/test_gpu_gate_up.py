@@ -128,6 +128,8 @@ CASES = [
     (65, 50, 64, 32, False, True, False),       # prefill
     (100, 6144, 1536, 32, False, True, False),  # E2B gate/up at M = 100: one-pass skinny over two 64-row x blocks
     (96, 40, 512, 64, False, False, True),      # skinny over two x blocks, group 64, bf16 dots, h bf16
+    (160, 300, 1024, 32, False, True, False),   # skinny over three x blocks
+    (250, 40, 512, 128, False, False, True),    # skinny over four x blocks, group 128, bf16 dots, h bf16
     (300, 130, 192, 64, False, False, False),   # prefill, h bf16
     (257, 17, 320, 32, False, True, True),      # prefill, bf16 dots
     (4096, 4096, 64, 32, False, True, False),   # prefill with two W blocks per wave

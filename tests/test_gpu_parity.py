@@ -324,7 +324,8 @@ def test_linear_gemv16_route(M, K, N):
     (65, 15360, 3840, 13),  # 64 < M <= 128: skinny form, two 64-row x blocks (one real row in the second), 2 parts
     (128, 6144, 1536, 5),   # E2B down at M = 128: skinny form, 24 W blocks x 2 x blocks x 4 parts
     (100, 4160, 1000, 1),   # K % 256 != 0 above M = 64: LDS prefill form, 13 parts
-    (200, 4096, 1000, 1),   # LDS form, ragged N, 16 parts
+    (200, 4096, 1000, 1),   # skinny form over four x blocks (8 real rows in the last), ragged N, 4 parts
+    (300, 4096, 1000, 1),   # M > 256: LDS form, ragged N, 16 parts
     (300, 1152, 700, 3),    # LDS form, two x blocks, K % 256 != 0, 9 parts of 2 steps
 ])
 def test_linear_splitk_route(M, K, N, step):
@@ -512,7 +513,7 @@ def test_graph_capture_replays_match_eager():
         del junk
 
 
-@pytest.mark.parametrize("M,K,N", [(8, 15360, 1000), (24, 1152, 700), (200, 2048, 700), (100, 2048, 700)])
+@pytest.mark.parametrize("M,K,N", [(8, 15360, 1000), (24, 1152, 700), (300, 2048, 700), (100, 2048, 700)])
 def test_splitk_graph_replays_match_eager(M, K, N):
     """The split-K route (main kernel + finalize over the caller's workspace; the
     skinny form with 15 parts, the 32x32 form with 9, the LDS prefill form with 16,
