@@ -320,7 +320,9 @@ int w4a16_gate_up_gelu(const void* x, int32_t x_dtype, const int32_t* pk_gate, c
 }
 
 size_t w4a16_lm_head_workspace_size(int64_t M, int64_t V, int64_t K, int32_t x_dtype, int32_t topk) {
-  if (M <= 0 || V <= 0 || K <= 0) return 0;
+  // the x planes need K > 0; the top-k candidates do not depend on K (at K == 0 the
+  // logits are zeros and the top-k still runs over them)
+  if (M <= 0 || V <= 0 || K < 0) return 0;
   const size_t split = x_split_bytes(M, K, x_dtype);
   if (topk <= 0) return split;
   return split + round_up((size_t)8 * (size_t)M * (size_t)w4l_topk_parts(V, topk) * (size_t)topk, 256);

@@ -228,13 +228,21 @@ __global__ void __launch_bounds__(256) dequant_kernel(const uint32_t* __restrict
 // ================================================================ f32 x split
 // x f32 [M, K] -> three bf16 planes [3][M][K] with x = t0 + t1 + t2 exactly:
 // t0, t1 take the top 8 significand bits of x and of the remainder (bit
-// truncation), t2 the remaining <= 8 bits.
+// truncation), t2 the remaining <= 8 bits.  A non-finite x goes whole into t0
+// (+-inf, or the quiet NaN 0x7FC0) with t1 = t2 = +0, so the dot sees exactly
+// the f32 dot's +-inf * w and NaN * w (inf - inf in the split would make NaN).
 __global__ void __launch_bounds__(256) split3_kernel(const float* __restrict__ x,
                                                      uint16_t* __restrict__ out, int64_t n) {
   const int64_t stride = (int64_t)gridDim.x * blockDim.x;
   for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += stride) {
     const float v = x[i];
     const uint32_t u = __float_as_uint(v);
+    if ((u & 0x7f800000u) == 0x7f800000u) {
+      out[i] = (u & 0x007fffffu) ? (uint16_t)0x7fc0u : (uint16_t)(u >> 16);
+      out[n + i] = 0;
+      out[2 * n + i] = 0;
+      continue;
+    }
     const float t0 = __uint_as_float(u & 0xffff0000u);
     const float r1 = v - t0;
     const float t1 = __uint_as_float(__float_as_uint(r1) & 0xffff0000u);

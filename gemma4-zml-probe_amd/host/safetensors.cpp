@@ -145,10 +145,27 @@ class Json {
 }  // namespace
 
 int64_t TensorInfo::numel() const {
+  // dims are checked non-negative and their product checked for overflow when the
+  // header is parsed (numel_checked), so this product fits
   int64_t n = 1;
   for (int64_t d : shape) n *= d;
   return n;
 }
+
+namespace {
+// Product of the dims times the element size, or false when it overflows 63 bits
+// (a crafted shape such as [2^62, 4] would otherwise wrap to a small byte count
+// and pass the data_offsets check).
+bool numel_checked(const std::vector<int64_t>& shape, size_t es, uint64_t* bytes) {
+  int64_t n = 1;
+  for (int64_t d : shape)
+    if (__builtin_mul_overflow(n, d, &n)) return false;
+  int64_t b;
+  if (__builtin_mul_overflow(n, (int64_t)es, &b)) return false;
+  *bytes = (uint64_t)b;
+  return true;
+}
+}  // namespace
 
 size_t dtype_size(const std::string& d) {
   if (d == "BOOL" || d == "U8" || d == "I8" || d == "F8_E4M3" || d == "F8_E5M2") return 1;
@@ -208,7 +225,9 @@ void SafeTensorsFile::parse_header(const std::string& json, uint64_t data_size, 
         if (d < 0) bad(name + ": negative dimension");
       const size_t es = dtype_size(t.dtype);
       if (es == 0) bad(name + ": unknown dtype " + t.dtype);
-      if ((uint64_t)t.numel() * es != t.end - t.begin) bad(name + ": data_offsets do not match shape x dtype");
+      uint64_t nbytes = 0;
+      if (!numel_checked(t.shape, es, &nbytes)) bad(name + ": shape x dtype overflows 64 bits");
+      if (nbytes != t.end - t.begin) bad(name + ": data_offsets do not match shape x dtype");
       if (t.end > data_size) bad(name + ": data_offsets past the end of the file");
       if (tensors.count(name)) bad(name + ": duplicate tensor name");
       tensors[name] = t;

@@ -117,6 +117,14 @@ size_t w4a16_workspace_size(int64_t M, int64_t N, int64_t K, int32_t x_dtype);
  * (RNE_bf16(q * s)); products with x are exact and accumulate in fp32, as in
  * dotPrec with fam = null (engine.zig:531-532).  Only the summation order
  * differs from the reference.
+ * Scale range: the in-register dequant is exact for 2^-126 <= |s| < 2^120 and
+ * s = +-0, which holds for every scale a quantizer writes (max|w| / 7.5 of a
+ * finite bf16 row group).  Outside it the fused kernels may differ from
+ * w4a16_dequant followed by a dot: a subnormal scale is flushed to zero (its
+ * group's weights count as 0), and from |s| >= 2^120 the expansion's fp32
+ * intermediate (128 + n) * s may overflow, so such scales (and +-inf / NaN
+ * ones) can give +-inf or NaN outputs.  w4a16_dequant is exact for every bit
+ * pattern.  The same holds for w4a16_linear_group and w4a16_gate_up_gelu.
  *   x_dtype  W4A16_DTYPE_BF16 or W4A16_DTYPE_F32 (the
  *            engine's f32 activations; carried exactly as a sum of three bf16
  *            terms, so no precision is lost before the fp32 accumulate).
@@ -206,9 +214,10 @@ int w4a16_gate_up_gelu(const void *x, int32_t x_dtype,
 
 /*
  * Bytes of device workspace w4a16_lm_head needs: the f32-activation split of
- * w4a16_workspace_size (x_dtype F32) plus 8 * M * ceil(V / S) * topk bytes of
- * top-k candidates, S = 1024 when ceil(V / 1024) * topk <= 4096 and 4096
- * otherwise (0 when topk is 0), rounded up to 256.
+ * w4a16_workspace_size (x_dtype F32, K > 0) plus 8 * M * ceil(V / S) * topk bytes
+ * of top-k candidates, S = 1024 when ceil(V / 1024) * topk <= 4096 and 4096
+ * otherwise (0 when topk is 0), rounded up to 256.  The candidate part does not
+ * depend on K: at K == 0 the logits are zeros and the top-k still runs.
  */
 size_t w4a16_lm_head_workspace_size(int64_t M, int64_t V, int64_t K, int32_t x_dtype, int32_t topk);
 

@@ -319,6 +319,9 @@ def test_lm_head_validation(L):
     assert _lm(L, ti=None) == w4a16.EINVAL_PTR
     assert _lm(L, ws=None, wsb=0) == w4a16.EWORKSPACE      # top-k candidates need workspace
     assert _lm(L, ws=A, wsb=64) == w4a16.EWORKSPACE
+    # K == 0 with top-k: the logits are zeros and the top-k still needs its candidates
+    # (the check returns before any HIP call)
+    assert _lm(L, V=100, K=0, ws=None, wsb=0) == w4a16.EWORKSPACE
     assert _lm(L, M=0, x=None, e=None, lg=None, tv=None, ti=None, ws=None, wsb=0) == 0
     assert L.w4a16_last_error().decode() == ""
 
@@ -330,6 +333,10 @@ def test_lm_head_workspace_size(L):
     assert L.w4a16_lm_head_workspace_size(1, 262144, 3840, w4a16.DTYPE_BF16, 64) == 64 * 64 * 8  # 4096-slices
     split = L.w4a16_workspace_size(2, 262144, 3840, w4a16.DTYPE_F32)
     assert L.w4a16_lm_head_workspace_size(2, 262144, 3840, w4a16.DTYPE_F32, 5) == split + 20480
+    # the candidates do not depend on K (K == 0 included); the x planes do
+    assert L.w4a16_lm_head_workspace_size(1, 100, 0, w4a16.DTYPE_BF16, 5) == 256
+    assert L.w4a16_lm_head_workspace_size(1, 100, 0, w4a16.DTYPE_F32, 5) == 256
+    assert L.w4a16_lm_head_workspace_size(1, 100, 0, w4a16.DTYPE_BF16, 0) == 0
 
 
 def test_linear_group_validation(L):

@@ -456,6 +456,31 @@ def test_linear_f32_activations():
         check_f32(y, x, w, K, x_f32=True)
 
 
+def test_linear_f32_activations_non_finite():
+    """+-inf and NaN in f32 x follow the f32 dot (engine.zig:531-532): +-inf * w (NaN where
+    w = +-0 or where infinities of both signs meet), NaN * w = NaN; the other rows are
+    untouched and meet the f32 bound."""
+    say("f32 activations with +-inf / NaN")
+    for M, K, N in [(1, 1536, 2048), (3, 3840, 512), (7, 3840, 512), (64, 256, 96)]:
+        _, pk, sc = o.synth_weights(N, K, 37)
+        rng = np.random.default_rng(100 + M)
+        x = rng.standard_normal((M, K), dtype=np.float32)
+        x[0, 5] = np.inf
+        x[0, K - 1] = np.inf
+        if M > 1:
+            x[1, 17] = -np.inf
+            x[M - 1, K // 2] = np.nan if M > 2 else x[M - 1, K // 2]
+        w = o.dequant(pk, sc)
+        y = gpu_linear(x, pk, sc, "f32", x_f32=True)
+        ref = o.matmul_f32x(x, w)
+        assert np.array_equal(np.isnan(y), np.isnan(ref)), (M, K, N)
+        inf = np.isinf(ref)
+        assert np.array_equal(np.isinf(y), inf) and np.array_equal(np.sign(y[inf]), np.sign(ref[inf]))
+        bad = ~np.isfinite(x).all(axis=1)
+        if (~bad).any():
+            check_f32(y[~bad], x[~bad], w, K, x_f32=True)
+
+
 def test_deterministic_and_stream_ordered():
     say("determinism + non-default stream")
     K, N = 3840, 4096

@@ -160,6 +160,18 @@ def test_empty_header_and_offsets_checked(tool, tmp_path):
     assert rc == 3 and "data_offsets" in err
 
 
+@pytest.mark.parametrize("shape", ["[4611686018427387904,4]", "[2147483648,2147483648,4]",
+                                   "[9223372036854775807,2]"])
+def test_overflowing_shape_rejected(tool, tmp_path, shape):
+    """A shape whose element count times the element size wraps 64 bits (e.g. [2^62, 4] of I8
+    would wrap to 0 bytes and pass the data_offsets check) is rejected before any use."""
+    path = tmp_path / "ovf.safetensors"
+    hdr = ('{"a.weight_packed":{"dtype":"I8","shape":%s,"data_offsets":[0,0]}}' % shape).encode()
+    path.write_bytes(len(hdr).to_bytes(8, "little") + hdr)
+    rc, _, err = run(tool, "census", str(path))
+    assert rc == 3 and "overflows" in err, err
+
+
 @pytest.mark.gpu
 @pytest.mark.parametrize("M,out", [(1, "bf16"), (5, "f32"), (70, "bf16"), (24, "f32")])
 def test_cpp_w4lin_linear_and_dequant_on_gpu(tool, tmp_path, M, out):

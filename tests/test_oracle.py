@@ -184,6 +184,83 @@ def test_linear_f64_error_bound_random():
     del rng, q
 
 
+def _f32_x_not_bf16(M: int, K: int, seed: int) -> np.ndarray:
+    """f32 activations whose low 16 bits are nonzero almost everywhere (not bf16-representable),
+    spread over several binades, as the engine's f32 residual stream carries them."""
+    rng = np.random.default_rng(seed)
+    x = (rng.standard_normal((M, K)) * 2.0 ** rng.integers(-6, 6, (M, K))).astype(np.float32)
+    assert np.mean((x.view(np.uint32) & 0xFFFF) != 0) > 0.99
+    return x
+
+
+def test_matmul_magnitudes_match_numpy():
+    """The sum |x||w| that sizes every gamma_K bound of the GPU tests, checked from both sides
+    against numpy's own float64 contraction of the absolute values: an inflated magnitude
+    would make every bound vacuous, a deflated one would reject correct kernels."""
+    _, pk, sc = o.synth_weights(96, 1024, 31)
+    w = o.dequant(pk, sc)
+    w64 = o.bf16_to_f32(w).astype(np.float64)
+    xb = o.synth_x(5, 1024, 32)
+    y, mag = o.matmul_f64(xb, w)
+    x64 = o.bf16_to_f32(xb).astype(np.float64)
+    assert np.allclose(mag, np.abs(x64) @ np.abs(w64).T, rtol=1e-13, atol=0)
+    assert np.allclose(y, x64 @ w64.T, rtol=1e-12, atol=1e-12)
+    xf = _f32_x_not_bf16(5, 1024, 33)
+    yf, magf = o.matmul_f32x(xf, w, f64=True)
+    xf64 = xf.astype(np.float64)
+    assert np.allclose(magf, np.abs(xf64) @ np.abs(w64).T, rtol=1e-13, atol=0)
+    # planted mistake: a magnitude built from |sum x w| instead of sum |x w| is smaller and must differ
+    assert np.max(np.abs(magf - np.abs(xf64 @ w64.T))) > 1.0
+
+
+def test_matmul_f32x_pinned_by_numpy_and_torch():
+    """The f32-activation contraction (dotPrec fam = null with an f32 lhs, engine.zig:530-533):
+    the float64 form equals numpy's float64 x64 @ w64.T (rtol 1e-12), and the fp32 form lies
+    within gamma_K * sum |x||w| of it, as does torch's own fp32 matmul of the same operands."""
+    _, pk, sc = o.synth_weights(80, 1536, 41)
+    w = o.dequant(pk, sc)
+    w64 = o.bf16_to_f32(w).astype(np.float64)
+    x = _f32_x_not_bf16(6, 1536, 42)
+    x64 = x.astype(np.float64)
+    y64, mag = o.matmul_f32x(x, w, f64=True)
+    ref64 = x64 @ w64.T
+    assert np.allclose(y64, ref64, rtol=1e-12, atol=1e-12)
+    y32 = o.matmul_f32x(x, w)
+    b = _gamma_bound(1536, mag)
+    assert np.all(np.abs(y32.astype(np.float64) - ref64) <= b)
+    yt = (torch.from_numpy(x) @ torch.from_numpy(o.bf16_to_f32(w)).T).numpy().astype(np.float64)
+    assert np.all(np.abs(yt - ref64) <= b)
+    # o.linear routes f32 x through the same contraction
+    assert np.array_equal(o.linear(x, pk, sc), y32)
+    # planted mistake: rounding x to bf16 before the f32 contraction must leave the bound
+    xr = o.bf16_to_f32(o.round_bf16(x))
+    y_bad = o.matmul_f32x(xr, w).astype(np.float64)
+    assert np.max(np.abs(y_bad - ref64) - b) > 0
+
+
+def test_matmul_f32x_non_finite_activations():
+    """IEEE f32 semantics of the f32-activation dot: +-inf in x gives +-inf times w (NaN where
+    w is +-0, or where infinities of both signs meet); NaN in x gives NaN."""
+    _, pk, sc = o.synth_weights(32, 256, 51)
+    w = o.dequant(pk, sc)
+    wf = o.bf16_to_f32(w).astype(np.float64)
+    x = _f32_x_not_bf16(3, 256, 52)
+    x[0, 7] = np.inf
+    x[1, 100] = -np.inf
+    x[2, 5] = np.nan
+    with np.errstate(invalid="ignore", over="ignore"):
+        ref = x.astype(np.float64) @ wf.T
+    y32 = o.matmul_f32x(x, w)
+    y64, _ = o.matmul_f32x(x, w, f64=True)
+    for y in (y32.astype(np.float64), y64):
+        assert np.array_equal(np.isnan(y), np.isnan(ref))
+        fin = ~np.isnan(ref)
+        assert np.array_equal(np.isinf(y[fin]), np.isinf(ref[fin]))
+        assert np.array_equal(np.sign(y[np.isinf(ref)]), np.sign(ref[np.isinf(ref)]))
+    assert np.all(np.isnan(y32[2]))
+    assert np.isnan(y32[0][wf[:, 7] == 0]).all() and np.isinf(y32[0][wf[:, 7] != 0]).all()
+
+
 def test_linear_one_hot_selects_a_column():
     q, pk, sc = o.synth_weights(48, 256, 21)
     w = o.dequant(pk, sc)
