@@ -362,19 +362,15 @@ hipError_t w4l_head_logits(const uint16_t* x_planes, int64_t xplane, int nterms,
   // 16-row form: the tile loop, ~1 workgroup per CU (2 when x fits in 64 KB)
   // each walking `per` tiles (at M = 16, V = 262144: 539 -> 415 us).  The 4-row
   // form keeps one workgroup per tile, which measured faster there (M = 1: 322
-  // against 350 us).  W4A16_HEAD_LOOP=0/1 overrides it for tuning.
-  bool loop = mr == 16;
-  if (const char* ev = getenv("W4A16_HEAD_LOOP")) loop = atoi(ev) != 0;
-  if (loop) {
+  // against 350 us).
+  if (mr == 16) {
     const int64_t ntiles = (V + 15) / 16;
-    int64_t nwg = lds > 65536 ? 256 : 512;
-    if (const char* e2 = getenv("W4A16_HEAD_WG")) nwg = atoll(e2);
-    if (nwg < 1) nwg = 1;
+    const int64_t nwg = lds > 65536 ? 256 : 512;
     const int per = (int)((ntiles + nwg - 1) / nwg);
     const dim3 grid((unsigned)((ntiles + per - 1) / per)), block(64 * waves);
 #define W4_HL(NT_, NST_, XPT_)                                                                       \
   do {                                                                                               \
-    auto k = mr == 16 ? w4k::head_loop_kernel<NT_, NST_, XPT_, 16> : w4k::head_loop_kernel<NT_, NST_, XPT_, 4>; \
+    auto k = w4k::head_loop_kernel<NT_, NST_, XPT_, 16>;                                              \
     if (lds > 65536 &&                                                                               \
         (err = hipFuncSetAttribute(reinterpret_cast<const void*>(k),                                 \
                                    hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024)) != hipSuccess) \

@@ -674,144 +674,6 @@ __global__ void __launch_bounds__(1024) gemv_fast_kernel(GemvArgs a) {
   }
 }
 
-// ---------------------------------------------------------------- GEMV, streaming variant
-// One workgroup per 16-row tile, W waves splitting K into equal ranges of
-// CPW chunks of NST steps.  Each wave streams its range with two register
-// buffers: the loads of chunk q+1 are issued before chunk q is dequantized,
-// and every load is unconditional in a straight-line loop body (the final
-// chunk is peeled), so the compiler's wait counts stay exact and the next
-// chunk is in flight during the current one's VALU work.  x is staged in LDS
-// as in gemv_fast_kernel.
-template <int NST>
-struct SChunk {
-  uint4 w[NST][VPL];
-  uint32_t s[NST];
-};
-
-template <int NT, int NST, int XPT, bool G32>
-__global__ void __launch_bounds__(1024) gemv_stream_kernel(GemvArgs a, int cpw) {
-  extern __shared__ __attribute__((aligned(16))) uint16_t lds[];
-  const int lane = threadIdx.x & 63;
-  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-  const int nwaves = blockDim.x >> 6;
-  const int r = lane & 15;
-  const int c = lane >> 4;
-  const int n0 = blockIdx.x * 16;
-  const int sw0 = wave * cpw * NST;  // first step of this wave
-
-  const int nvec = (NT * a.M * a.K) >> 3;
-  const uint4* xsrc = reinterpret_cast<const uint4*>(a.x);
-  uint4 xv[XPT];
-  int xi[XPT];
-#pragma unroll
-  for (int i = 0; i < XPT; ++i) {
-    xi[i] = min((int)threadIdx.x + i * (int)blockDim.x, nvec - 1);
-    xv[i] = xsrc[xi[i]];
-  }
-
-  const int nrow = min(n0 + r, a.N - 1);
-  const uint32_t* pkrow = a.pk + (int64_t)nrow * (a.K >> 3);
-  const uint16_t* scrow = a.sc + (int64_t)nrow * a.groups_per_row;
-  auto load = [&](SChunk<NST>& b, int q) {
-#pragma unroll
-    for (int i = 0; i < NST; ++i) {
-      const int g0 = ((sw0 + q * NST + i) * 4 + c) * VPL;
-#pragma unroll
-      for (int v = 0; v < VPL; ++v) b.w[i][v] = *reinterpret_cast<const uint4*>(pkrow + 4 * (g0 + v));
-      if (G32) b.s[i] = *reinterpret_cast<const uint32_t*>(scrow + g0);
-      else b.s[i] = (uint32_t)scrow[g0 / a.group_chunks] | ((uint32_t)scrow[(g0 + 1) / a.group_chunks] << 16);
-    }
-  };
-  SChunk<NST> bA, bB;
-  load(bA, 0);
-
-  uint4* xdst = reinterpret_cast<uint4*>(lds);
-#pragma unroll
-  for (int i = 0; i < XPT; ++i) xdst[xi[i]] = xv[i];
-  __syncthreads();
-
-  uint32_t kM = 0x000F000Fu, kO = 0x43004300u;
-  asm volatile("" : "+v"(kM), "+v"(kO));
-  floatx4 acc[1] = {floatx4{0.f, 0.f, 0.f, 0.f}};
-  const int plane = a.M * a.K;
-  const uint16_t* xrow = lds + min(r, a.M - 1) * a.K;
-  auto compute = [&](const SChunk<NST>& b, int q) {
-#pragma unroll
-    for (int i = 0; i < NST; ++i) {
-#pragma unroll
-      for (int v = 0; v < VPL; ++v) {
-        const int g = ((sw0 + q * NST + i) * 4 + c) * VPL + v;
-        const uint32_t slo = v == 0 ? (b.s[i] & 0xffffu) : (b.s[i] >> 16);
-        const uint32_t shi = slo << 16;
-        const float cneg = -136.0f * __uint_as_float(shi);
-        const uint16_t* xr = xrow + 32 * g;
-        const uint32_t wj[4] = {b.w[i][v].x, b.w[i][v].y, b.w[i][v].z, b.w[i][v].w};
-#pragma unroll
-        for (int j = 0; j < 4; ++j) {
-          const bf16x8 bb = dequant8(wj[j], slo, shi, cneg, kM, kO);
-#pragma unroll
-          for (int t = 0; t < NT; ++t)
-            mfma_acc(acc[0], *reinterpret_cast<const bf16x8*>(xr + t * plane + 8 * j), bb);
-        }
-      }
-    }
-    mfma_drain<1>(acc);
-  };
-  // sched_barrier(0) keeps the scheduler from sinking the next chunk's loads
-  // into the current chunk's compute (it would then wait for them).
-  int q = 0;
-  for (; q + 2 < cpw; q += 2) {
-    load(bB, q + 1);
-    __builtin_amdgcn_sched_barrier(0);
-    compute(bA, q);
-    __builtin_amdgcn_sched_barrier(0);
-    load(bA, q + 2);
-    __builtin_amdgcn_sched_barrier(0);
-    compute(bB, q + 1);
-    __builtin_amdgcn_sched_barrier(0);
-  }
-  if (q + 1 < cpw) {
-    load(bB, q + 1);
-    __builtin_amdgcn_sched_barrier(0);
-    compute(bA, q);
-    __builtin_amdgcn_sched_barrier(0);
-    compute(bB, q + 1);
-  } else {
-    compute(bA, q);
-  }
-  mfma_drain<1>(acc);
-
-  if (nwaves == 1) {
-    if (c == 0 && r < 16) {
-#pragma unroll
-      for (int m = 0; m < 4; ++m) {
-        const int n = n0 + r;
-        if (m < a.M && n < a.N) {
-          if (a.y_f32) reinterpret_cast<float*>(a.y)[(int64_t)m * a.N + n] = acc[0][m];
-          else reinterpret_cast<uint16_t*>(a.y)[(int64_t)m * a.N + n] = (uint16_t)f32_to_bf16_rne(acc[0][m]);
-        }
-      }
-    }
-    return;
-  }
-  float* red = reinterpret_cast<float*>(lds + NT * plane);
-  if (c == 0) {
-#pragma unroll
-    for (int i = 0; i < 4; ++i) red[(wave * 4 + i) * 16 + r] = acc[0][i];
-  }
-  __syncthreads();
-  if ((int)threadIdx.x < 16 * a.M) {
-    const int m = threadIdx.x >> 4, rr = threadIdx.x & 15;
-    float v = 0.f;
-    for (int w = 0; w < nwaves; ++w) v += red[(w * 4 + m) * 16 + rr];
-    const int n = n0 + rr;
-    if (n < a.N) {
-      if (a.y_f32) reinterpret_cast<float*>(a.y)[(int64_t)m * a.N + n] = v;
-      else reinterpret_cast<uint16_t*>(a.y)[(int64_t)m * a.N + n] = (uint16_t)f32_to_bf16_rne(v);
-    }
-  }
-}
-
 // ---------------------------------------------------------------- skinny / prefill linear
 // M > 4, bf16 x, K % 256 == 0.  A workgroup of 4 waves owns 64 rows of W (16 per
 // wave) and 16*MT rows of x, and walks K in chunks of 256 columns.  Per chunk:
@@ -1627,15 +1489,14 @@ hipError_t w4l_fill_zero(void* p, int64_t bytes, hipStream_t st) {
 bool w4l_gemv16_plan(int64_t M, int64_t N, int64_t K, int nterms, int* nst_out, int* waves_out, int* xpt_out);
 // M <= 16 through the 16-row GEMV (for M <= 4 where the 4-row plan does not
 // hold) when its plan holds and every 16-row tile
-// re-reading x from L2 stays under 40 MiB (W4A16_GEMV16_XBYTES overrides):
+// re-reading x from L2 stays under 40 MiB:
 // measured on the 12B and E2B rows, the GEMV wins 1.2-1.9x below that (q, k/v, o,
 // E2B) and the skinny kernel, whose workgroups share x over 64-128 rows, wins
 // above it (12B gate/up, full-layer q at M = 16).
 bool w4l_gemv16_ok(int64_t M, int64_t N, int64_t K, int nterms) {
   int nst, waves, xpt;
   if (!w4l_gemv16_plan(M, N, K, nterms, &nst, &waves, &xpt)) return false;
-  int64_t max_bytes = 40ll << 20;
-  if (const char* e = getenv("W4A16_GEMV16_XBYTES")) max_bytes = atoll(e);
+  const int64_t max_bytes = 40ll << 20;
   return (N + 15) / 16 * M * K * 2 <= max_bytes;
 }
 
@@ -1662,20 +1523,13 @@ bool w4l_gemv_fast_plan(int64_t M, int64_t N, int64_t K, int nterms, int* nst_ou
   // wave streams best when it divides K/256, then two, four, one
   static const int pref[] = {5, 2, 4, 1, 3, 6};
   int nst = 0, waves = 0;
-  // W4A16_GEMV_NST=<1..6>: tuning override of the steps per wave, when it divides
-  if (const char* e = getenv("W4A16_GEMV_NST")) {
-    const int p = atoi(e);
-    if (p >= 1 && p <= 6 && steps % p == 0 && steps / p <= 16) { nst = p; waves = (int)(steps / p); }
-  }
   for (int p : pref) {
     if (nst) break;
     if (steps % p == 0 && steps / p <= 16) { nst = p; waves = (int)(steps / p); break; }
   }
   if (!nst) return false;
-  // one 16-row tile per workgroup; two (W4A16_GEMV_TPW=2) measured slower on
-  // every decode shape but stays available for tuning
-  int tpw = 1;
-  if (const char* e = getenv("W4A16_GEMV_TPW")) tpw = atoi(e) == 2 ? 2 : 1;
+  // one 16-row tile per workgroup (two measured slower on every decode shape)
+  const int tpw = 1;
   const int64_t nvec = (int64_t)nterms * M * K / 8;
   const int64_t per = (nvec + 64 * waves - 1) / (64 * waves);
   int xpt = 1;
@@ -1691,11 +1545,8 @@ bool w4l_gemv_fast_plan(int64_t M, int64_t N, int64_t K, int nterms, int* nst_ou
 // Straight-line GEMV for 4 < M <= 16 (bf16 x): the same kernel with a 16-row
 // epilogue.  As many waves as K / 256 allows (<= 16) so that each thread stages
 // at most 8 x vectors; x [M][K] sits in LDS whole (up to 160 KB on gfx950).
-// W4A16_GEMV16=0 turns the route off (tuning).
 bool w4l_gemv16_plan(int64_t M, int64_t N, int64_t K, int nterms, int* nst_out, int* waves_out, int* xpt_out) {
   if (nterms != 1 || M < 1 || M > 16 || K % w4k::GSTEP != 0 || N <= 0) return false;
-  if (const char* e = getenv("W4A16_GEMV16"))
-    if (atoi(e) == 0) return false;
   const int64_t steps = K / w4k::GSTEP;
   int nst = 0;
   for (int p = 1; p <= 6 && !nst; ++p)
@@ -1711,42 +1562,6 @@ bool w4l_gemv16_plan(int64_t M, int64_t N, int64_t K, int nterms, int* nst_out, 
   if (lds > 160 * 1024) return false;
   *nst_out = nst;
   *waves_out = waves;
-  *xpt_out = xpt;
-  return true;
-}
-
-// Streaming GEMV plan (opt-in with W4A16_GEMV_STREAM): waves per tile W,
-// chunk steps NST, chunks per wave CPW with W * CPW * NST == K / GSTEP.  Few
-// tiles -> more waves per tile.  W4A16_GEMV_W / W4A16_GEMV_NST override.
-bool w4l_gemv_stream_plan(int64_t M, int64_t N, int64_t K, int nterms, int* w_out, int* nst_out,
-                          int* cpw_out, int* xpt_out) {
-  if (K % w4k::GSTEP != 0) return false;
-  const int64_t steps = K / w4k::GSTEP;
-  const int64_t tiles = (N + 15) / 16;
-  int64_t want_w = (2048 + tiles - 1) / tiles;  // >= ~2048 waves in the grid
-  if (want_w > 16) want_w = 16;
-  if (const char* e = getenv("W4A16_GEMV_W")) want_w = atoi(e);
-  int pref_nst = 3;
-  if (const char* e = getenv("W4A16_GEMV_NST")) pref_nst = atoi(e);
-  int w = 0, nst = 0;
-  for (int64_t cw = want_w < 1 ? 1 : want_w; cw <= 16 && !w; ++cw)
-    if (steps % cw == 0) w = (int)cw;
-  if (!w) return false;
-  const int64_t per = steps / w;
-  static const int order[] = {3, 4, 2, 5, 6, 1};
-  if (pref_nst >= 1 && pref_nst <= 6 && per % pref_nst == 0) nst = pref_nst;
-  for (int o : order) {
-    if (nst) break;
-    if (per % o == 0) nst = o;
-  }
-  const int64_t nvec = (int64_t)nterms * M * K / 8;
-  const int64_t xper = (nvec + 64 * w - 1) / (64 * w);
-  int xpt = 1;
-  while (xpt < xper) xpt *= 2;
-  if (xpt > 8) return false;
-  *w_out = w;
-  *nst_out = nst;
-  *cpw_out = (int)(per / nst);
   *xpt_out = xpt;
   return true;
 }
@@ -1809,11 +1624,7 @@ static hipError_t gemv_fast_launch(const w4k::GemvArgs& a, int nterms, int nst, 
     if (g32) hipLaunchKernelGGL((w4k::gemv_fast_kernel<NT_, NST_, XPT_, TPW_, true>), grid, block, lds, st, a); \
     else hipLaunchKernelGGL((w4k::gemv_fast_kernel<NT_, NST_, XPT_, TPW_, false>), grid, block, lds, st, a);    \
   } while (0)
-#define W4_FAST_T(NT_, NST_, XPT_)                        \
-  do {                                                    \
-    if (tpw == 2) W4_FAST(NT_, NST_, XPT_, 2);            \
-    else W4_FAST(NT_, NST_, XPT_, 1);                     \
-  } while (0)
+#define W4_FAST_T(NT_, NST_, XPT_) W4_FAST(NT_, NST_, XPT_, 1)
 #define W4_FAST_X(NT_, NST_)                    \
   switch (xpt) {                                \
     case 1: W4_FAST_T(NT_, NST_, 1); break;     \
@@ -1872,52 +1683,6 @@ hipError_t w4l_gemv(const uint16_t* x_planes, int nterms, const int32_t* pk, con
       a.bf16_dots = pair->bf16_dots;
     }
     return gemv16_launch(a, nst, waves, xpt, (int)((N + 15) / 16), group == 32, st);
-  }
-  if (!pair && getenv("W4A16_GEMV_STREAM")) {
-    int w, nst, cpw, xpt;
-    if (w4l_gemv_stream_plan(M, N, K, nterms, &w, &nst, &cpw, &xpt)) {
-      w4k::GemvArgs a{};
-      a.x = x_planes;
-      a.pk = reinterpret_cast<const uint32_t*>(pk);
-      a.sc = sc;
-      a.y = y;
-      a.M = (int)M;
-      a.N = (int)N;
-      a.K = (int)K;
-      a.group_chunks = group / 32;
-      a.groups_per_row = (int)(K / group);
-      a.y_f32 = y_f32;
-      a.steps = (int)(K / w4k::GSTEP);
-      const size_t lds = (size_t)nterms * M * K * 2 + (size_t)w * 4 * 16 * 4;
-      const dim3 grid((unsigned)((N + 15) / 16)), block(64 * w);
-      const bool g32 = group == 32;
-#define W4_ST(NT_, NST_, XPT_)                                                                             \
-  do {                                                                                                     \
-    if (g32) hipLaunchKernelGGL((w4k::gemv_stream_kernel<NT_, NST_, XPT_, true>), grid, block, lds, st, a, cpw); \
-    else hipLaunchKernelGGL((w4k::gemv_stream_kernel<NT_, NST_, XPT_, false>), grid, block, lds, st, a, cpw);    \
-  } while (0)
-#define W4_ST_X(NT_, NST_)                 \
-  switch (xpt) {                           \
-    case 1: W4_ST(NT_, NST_, 1); break;    \
-    case 2: W4_ST(NT_, NST_, 2); break;    \
-    case 4: W4_ST(NT_, NST_, 4); break;    \
-    default: W4_ST(NT_, NST_, 8); break;   \
-  }
-#define W4_ST_N(NT_)                       \
-  switch (nst) {                           \
-    case 1: W4_ST_X(NT_, 1); break;        \
-    case 2: W4_ST_X(NT_, 2); break;        \
-    case 3: W4_ST_X(NT_, 3); break;        \
-    case 4: W4_ST_X(NT_, 4); break;        \
-    case 5: W4_ST_X(NT_, 5); break;        \
-    default: W4_ST_X(NT_, 6); break;       \
-  }
-      if (nterms == 1) { W4_ST_N(1) } else { W4_ST_N(3) }
-#undef W4_ST_N
-#undef W4_ST_X
-#undef W4_ST
-      return hipGetLastError();
-    }
   }
   {
     int nst, waves, xpt, tpw;
@@ -2024,19 +1789,12 @@ hipError_t w4l_skinny(const uint16_t* x, const int32_t* pk, const uint16_t* sc, 
   a.nk = (int)(K / 256 / kq);
   a.kq = kq;
   a.part = part;
-  int mt = M <= 16 ? 1 : M <= 32 ? 2 : 4;
-  // W4A16_SKINNY_MT=<1|2|4>: tuning override of the 16-row x tiles per workgroup
-  if (const char* e = getenv("W4A16_SKINNY_MT")) {
-    const int v = atoi(e);
-    if (v == 1 || v == 2 || v == 4) mt = v;
-  }
+  const int mt = M <= 16 ? 1 : M <= 32 ? 2 : 4;
   // Eight waves (128 W rows) per workgroup when that still gives >= 240
   // workgroups: x is then re-read from L2 half as often (12B gate/up, M = 64:
   // 36.6 -> 30.7 us; M = 16 / 32: 22.0 / 26.6 -> 19.8 / 23.1).  Smaller N keeps
-  // four waves so the grid still fills the GPU.  W4A16_SKINNY_NW=<4|8> overrides
-  // it for tuning.
-  int nw = ((N + 127) / 128) * ((M + 16 * mt - 1) / (16 * mt)) * kq >= 240 ? 8 : 4;
-  if (const char* e = getenv("W4A16_SKINNY_NW")) nw = atoi(e) == 8 ? 8 : 4;
+  // four waves so the grid still fills the GPU.
+  const int nw = ((N + 127) / 128) * ((M + 16 * mt - 1) / (16 * mt)) * kq >= 240 ? 8 : 4;
   const dim3 grid((unsigned)((N + 16 * nw - 1) / (16 * nw)), (unsigned)((M + 16 * mt - 1) / (16 * mt)),
                   (unsigned)kq),
       block(64 * nw);
@@ -2101,56 +1859,22 @@ hipError_t w4l_prefill(const uint16_t* x, const int32_t* pk, const uint16_t* sc,
   a.y_f32 = y_f32;
   a.ns = (int)(K / 64);
   a.kq = 1;
-  // x rows per workgroup: 32 / 64 / 128 / 256 (MB = 1 / 2 / 4 / 8 blocks of 32), the
-  // smallest that holds M, so small M pays no MFMAs on padding rows
-  const int mb = M <= 32 ? 1 : M <= 64 ? 2 : M <= 128 ? 4 : 8;
+  // x rows per workgroup: 128 / 256 (MB = 4 / 8 blocks of 32; M > 64 here), the
+  // smallest that holds M, so M <= 128 pays no MFMAs on padding rows
+  if (M <= 64) return hipErrorInvalidValue;
+  const int mb = M <= 128 ? 4 : 8;
   a.mblk = (int)((M + 32 * mb - 1) / (32 * mb));
-  if (mb <= 2) {
-    // the skinny regime: WS waves of W rows x a K split KS (tuning overrides
-    // W4A16_PF_WS=<2|4>, W4A16_PF_KS=<1|2|4>)
-    int ws = 4, ks = 2;
-    if (const char* e = getenv("W4A16_PF_WS")) ws = atoi(e) == 2 ? 2 : 4;
-    if (const char* e = getenv("W4A16_PF_KS")) ks = atoi(e);
-    if (ks != 1 && ks != 2 && ks != 4) ks = 2;
-    if (ws == 4 && ks == 4) ks = 2;
-    while (ks > 1 && K % (64 * ks) != 0) ks /= 2;
-    a.ns = (int)(K / (64 * ks));
-    const int bn = ws * 32;
-    const dim3 grid((unsigned)(((N + bn - 1) / bn) * a.mblk)), block(64 * ws * ks);
-    const bool g32 = group == 32;
-#define W4_PFS(MB_, WS_, KS_)                                                                                \
-  do {                                                                                                       \
-    if (g32) hipLaunchKernelGGL((w4k::prefill_kernel<1, 4, true, MB_, WS_, KS_>), grid, block, 0, st, a);   \
-    else hipLaunchKernelGGL((w4k::prefill_kernel<1, 4, false, MB_, WS_, KS_>), grid, block, 0, st, a);      \
-  } while (0)
-#define W4_PFS_M(WS_, KS_)          \
-  do {                              \
-    if (mb == 1) W4_PFS(1, WS_, KS_); \
-    else W4_PFS(2, WS_, KS_);         \
-  } while (0)
-    if (ws == 4 && ks == 1) W4_PFS_M(4, 1);
-    else if (ws == 4) W4_PFS_M(4, 2);
-    else if (ks == 1) W4_PFS_M(2, 1);
-    else if (ks == 2) W4_PFS_M(2, 2);
-    else W4_PFS_M(2, 4);
-#undef W4_PFS_M
-#undef W4_PFS
-    return hipGetLastError();
-  }
   // W expanded into LDS, 8 waves (two per SIMD): 256 x 256 tiles when they still
   // give >= 240 workgroups, else 256 x 128.  Measured on the 12B / E2B shapes, us,
   // against the one-wave-per-SIMD kernel below: 256 x 256 gate/up at M = 512 /
   // 1024 / 2048 / 4096 167 / 327 / 536 / 1066 -> 133 / 257 / 510 / 1019, down at
   // M = 4096 569 -> 457; 256 x 128 down at M = 1024 / 2048 287 / 293 -> 249 / 279,
   // full-layer o 163 -> 152, E2B down 124 -> 105 (the 256 x 256 tile gives those
-  // 60-120 workgroups and took 224-416).  W4A16_PF_LDS=0/1/2 overrides the choice
-  // (one-wave kernel / 128 / 256 W rows; tuning).
-  int lds_tn = ((N + 255) / 256) * a.mblk >= 240 ? 2 : 1;
-  if (const char* ev = getenv("W4A16_PF_LDS")) lds_tn = atoi(ev);
-  if (mb == 8 && (lds_tn == 1 || lds_tn == 2)) return prefill_lds_launch(a, lds_tn, group == 32, st);
-  // two W blocks of 32 rows per wave when that still leaves two workgroups per CU
-  const bool tn2 = mb == 8 && ((N + 255) / 256) * a.mblk >= 512;
-  const int bn = tn2 ? 256 : 128;
+  // 60-120 workgroups and took 224-416).
+  const int lds_tn = ((N + 255) / 256) * a.mblk >= 240 ? 2 : 1;
+  if (mb == 8) return prefill_lds_launch(a, lds_tn, group == 32, st);
+  // 64 < M <= 128: the one-wave kernel over 128-row x tiles
+  const int bn = 128;
   const dim3 grid((unsigned)(((N + bn - 1) / bn) * a.mblk)), block(256);
   const bool g32 = group == 32;
 #define W4_PF(TN_, P_, MB_)                                                                         \
@@ -2158,20 +1882,14 @@ hipError_t w4l_prefill(const uint16_t* x, const int32_t* pk, const uint16_t* sc,
     if (g32) hipLaunchKernelGGL((w4k::prefill_kernel<TN_, P_, true, MB_>), grid, block, 0, st, a);  \
     else hipLaunchKernelGGL((w4k::prefill_kernel<TN_, P_, false, MB_>), grid, block, 0, st, a);     \
   } while (0)
-  if (tn2) W4_PF(2, 2, 8);
-  else if (mb == 8) W4_PF(1, 4, 8);
-  else if (mb == 4) W4_PF(1, 4, 4);
-  else W4_PF(1, 4, 2);
+  W4_PF(1, 4, 4);
 #undef W4_PF
   return hipGetLastError();
 }
 
 // Upper bound of the rows above 64 that the skinny kernel takes in several
-// 64-row x blocks (W4A16_SKINNY_MID=<M>, tuning; 0 turns it off).
-static int64_t skinny_mid_max() {
-  if (const char* e = getenv("W4A16_SKINNY_MID")) return atoll(e);
-  return 256;
-}
+// 64-row x blocks.
+static int64_t skinny_mid_max() { return 256; }
 
 // Split-K plan (bf16 x) for the shapes whose one-pass grid cannot fill the GPU.
 // Above M = 64: the skinny form up to M = 128 when K % 256 == 0, and up to 256
@@ -2196,9 +1914,8 @@ static int64_t skinny_mid_max() {
 //    M > 32, 128 for M <= 32; x blocks of 64 / 32 rows) and kq parts, the
 //    smallest divisor of K / 64 (<= 16) that gives >= 240 workgroups, else the
 //    largest.
-// Both cost kq f32 partial planes and one finalize pass.  W4A16_SPLITK=0 turns
-// the route off, W4A16_SPLITK_SKINNY=0 the skinny form, and W4A16_PF_KQ=<q>
-// forces the part count when it divides (tuning).
+// Both cost kq f32 partial planes and one finalize pass.  The plan, and so the
+// workspace size, is a function of (M, N, K) only.
 namespace {
 enum SplitForm { SPLIT_SKINNY, SPLIT_PF32, SPLIT_LDS };
 struct SplitPlan {
@@ -2218,11 +1935,7 @@ bool splitk_plan(int64_t M, int64_t N, int64_t K, int nterms, SplitPlan* p) {
     // 4096 at M = 160 17.8 / 26.1 -> 11.2 / 21.4 us, E2B down 23.7 -> 17.0, but
     // 12B down 48.8 against 72.5 and the E2B model projection (K = 15360) 30.8
     // against 41.6 at M = 256, where the LDS form splits K into more parts
-    bool sk = K % 256 == 0 && M <= skinny_mid_max() && (M <= 128 || K <= 8192);
-    if (const char* e = getenv("W4A16_SPLITK_SKINNY"))
-      if (atoi(e) == 0) sk = false;
-    if (const char* e = getenv("W4A16_SPLITK"))
-      if (atoi(e) == 0) return false;
+    const bool sk = K % 256 == 0 && M <= skinny_mid_max() && (M <= 128 || K <= 8192);
     if (sk) {
       const int64_t nk = K / 256;
       const int64_t per_part = ((N + 63) / 64) * ((M + 63) / 64);
@@ -2246,10 +1959,6 @@ bool splitk_plan(int64_t M, int64_t N, int64_t K, int nterms, SplitPlan* p) {
     if (M <= 128 && N > 8192) return false;
     const int64_t steps = K / 64;
     int q = 0;
-    if (const char* e = getenv("W4A16_PF_KQ")) {
-      const int v = atoi(e);
-      if (v >= 2 && v <= 16 && steps % v == 0) q = v;
-    }
     for (int c = 16; !q && c >= 2; --c)
       if (steps % c == 0 && grid * c <= 256) q = c;
     if (q < 2) return false;
@@ -2259,20 +1968,12 @@ bool splitk_plan(int64_t M, int64_t N, int64_t K, int nterms, SplitPlan* p) {
   if (N >= 16384) return false;
   if (M <= 4 && (w4l_gemv_ok(M, K, nterms) || K % 256 != 0)) return false;
   if (M > 4 && M <= 16 && (w4l_gemv16_ok(M, N, K, nterms) || (K < 8192 && N >= 8192))) return false;
-  if (const char* e = getenv("W4A16_SPLITK"))
-    if (atoi(e) == 0) return false;
-  int force = 0;
-  if (const char* e = getenv("W4A16_PF_KQ")) force = atoi(e);
-  bool try_skinny = K % 256 == 0;
-  if (const char* e = getenv("W4A16_SPLITK_SKINNY"))
-    if (atoi(e) == 0) try_skinny = false;
-  if (try_skinny) {
+  if (K % 256 == 0) {
     const int64_t nk = K / 256;
     const int64_t mt = M <= 16 ? 1 : M <= 32 ? 2 : 4;
     const int64_t per_part = ((N + 63) / 64) * ((M + 16 * mt - 1) / (16 * mt));
     int q = 0;
-    if (force >= 2 && force <= 64 && nk % force == 0) q = force;
-    for (int c = 2; !force && c <= nk && c <= 64; ++c)
+    for (int c = 2; c <= nk && c <= 64; ++c)
       if (nk % c == 0 && per_part * c <= 256) q = c;
     if (q >= 2) {
       *p = SplitPlan{SPLIT_SKINNY, q, 0, 0};
@@ -2288,7 +1989,6 @@ bool splitk_plan(int64_t M, int64_t N, int64_t K, int nterms, SplitPlan* p) {
   const int64_t tiles = (N + 32 * ws - 1) / (32 * ws);
   const int64_t steps = K / 64;
   int q = 0;
-  if (force >= 1 && force <= 16 && steps % force == 0) q = force;
   for (int c = 2; !q && c <= 16; ++c)
     if (steps % c == 0 && tiles * c >= 240) q = c;
   if (!q) {
@@ -2394,9 +2094,6 @@ hipError_t w4l_linear(const uint16_t* x_planes, int nterms, const int32_t* pk, c
   if (w4l_gemv_ok(M, K, nterms)) return w4l_gemv(x_planes, nterms, pk, sc, y, y_f32, M, N, K, group, st);
   if (skinny_mid(M, N, K, nterms)) return w4l_skinny(x_planes, pk, sc, y, y_f32, M, N, K, group, st);
   if (w4l_prefill_ok(M, K, nterms)) return w4l_prefill(x_planes, pk, sc, y, y_f32, M, N, K, group, st);
-  // W4A16_PF_SMALL=1: tuning switch, 4 < M <= 64 through the 32x32 kernel
-  if (getenv("W4A16_PF_SMALL") && nterms == 1 && M > 4 && K % 64 == 0)
-    return w4l_prefill(x_planes, pk, sc, y, y_f32, M, N, K, group, st);
   if (w4l_skinny_ok(M, K, nterms)) return w4l_skinny(x_planes, pk, sc, y, y_f32, M, N, K, group, st);
   const W4Plan p = w4l_plan(M, N, K, nterms);
   w4k::LinearArgs a{};
@@ -2448,7 +2145,6 @@ PairRoute pair_route(int64_t M, int64_t F, int64_t K, int nterms) {
   if (w4l_gemv16_ok(M, 16 * ((F + 7) / 8), K, nterms)) return PAIR_GEMV;
   if (skinny_mid(M, 16 * ((F + 7) / 8), K, nterms)) return PAIR_SKINNY;
   if (w4l_prefill_ok(M, K, nterms)) return PAIR_PREFILL;
-  if (getenv("W4A16_PF_SMALL") && nterms == 1 && M > 4 && K % 64 == 0) return PAIR_PREFILL;
   if (nterms == 1 && K % 256 == 0) return PAIR_SKINNY;
   return PAIR_NONE;
 }

@@ -34,7 +34,6 @@ bool w4l_gemv_ok(int64_t M, int64_t K, int nterms);
 // 4 < M <= 16 through the same GEMV kernel (bf16 x, small N); w4l_gemv takes it.
 bool w4l_gemv16_ok(int64_t M, int64_t N, int64_t K, int nterms);
 int w4l_gemv_waves(int64_t N, int64_t K);
-bool w4l_gemv_stream_plan(int64_t M, int64_t N, int64_t K, int nterms, int* w, int* nst, int* cpw, int* xpt);
 bool w4l_gemv_fast_plan(int64_t M, int64_t N, int64_t K, int nterms, int* nst, int* waves, int* xpt, int* tpw);
 // With a pair, only the straight-line plan is used (hipErrorInvalidValue when
 // w4l_gemv_fast_plan fails) and N is ignored.

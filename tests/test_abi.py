@@ -219,6 +219,38 @@ def test_workspace_size_splitk(L, M, N, K, expect):
     assert L.w4a16_workspace_size(M, N, K, w4a16.DTYPE_F32) == planes
 
 
+_TUNING_ENV = ("W4A16_GEMV16_XBYTES", "W4A16_GEMV_NST", "W4A16_GEMV_TPW", "W4A16_GEMV16", "W4A16_GEMV_W",
+               "W4A16_GEMV_STREAM", "W4A16_SKINNY_MT", "W4A16_SKINNY_NW", "W4A16_PF_WS", "W4A16_PF_KS",
+               "W4A16_PF_LDS", "W4A16_SKINNY_MID", "W4A16_SPLITK_SKINNY", "W4A16_SPLITK", "W4A16_PF_KQ",
+               "W4A16_PF_SMALL", "W4A16_HEAD_LOOP", "W4A16_HEAD_WG")
+
+
+def test_dispatch_reads_no_environment():
+    """Route and workspace size are functions of (M, N, K, group, dtypes) only: the library
+    imports no getenv, and every workspace size is the same in a process where all the
+    former tuning variables are set."""
+    import subprocess
+    import sys
+    syms = subprocess.run(["nm", "-D", "--undefined-only", w4a16.LIB_PATH], capture_output=True, text=True,
+                          check=True).stdout
+    assert not re.search(r"\bgetenv\b|secure_getenv", syms)
+    code = ("import sys, json; sys.path.insert(0, %r); import w4a16; L = w4a16.lib(); out = []\n"
+            "for M in (1, 3, 4, 8, 16, 17, 32, 64, 65, 96, 128, 160, 256, 300, 1024, 2048):\n"
+            "  for N, K in ((3840, 15360), (4096, 3840), (2048, 3840), (30720, 3840), (1536, 6144),\n"
+            "               (12288, 1536), (700, 1152), (1000, 4160), (8192, 3840)):\n"
+            "    for xd in (0, 1):\n"
+            "      out.append(L.w4a16_workspace_size(M, N, K, xd))\n"
+            "      out.append(L.w4a16_gate_up_workspace_size(M, N // 2, K, xd))\n"
+            "print(json.dumps(out))\n") % os.path.dirname(os.path.dirname(w4a16.__file__))
+    clean = {k: v for k, v in os.environ.items() if not k.startswith("W4A16_")}
+    runs = []
+    for env in (clean, dict(clean, **{k: "1" for k in _TUNING_ENV}),
+                dict(clean, **{k: "0" for k in _TUNING_ENV})):
+        runs.append(subprocess.run([sys.executable, "-c", code], env=env, capture_output=True, text=True,
+                                   check=True).stdout)
+    assert runs[0] == runs[1] == runs[2]
+
+
 def test_python_wrapper_refuses_cpu_tensors():
     import torch
     pk = torch.zeros((16, 8), dtype=torch.int32)
