@@ -162,6 +162,66 @@ __device__ __forceinline__ bf16x8 dequant8(uint32_t w, uint32_t slo, uint32_t sh
   return __builtin_bit_cast(bf16x8, r);
 }
 
+// 8 nibbles -> the same 8 bf16 weights RNE(q * s), written in C so that the
+// compiler schedules it and tracks every hazard (used by the decode GEMV).
+// Nibbles become f16 values placed by one v_bitop3 per pair:
+//   h0 = (w & 0x000F000F) | 0x64006400 = (1024 + n0, 1024 + n4)
+//   h1 = (w & 0x00F000F0) | 0x64006400 = (1024 + 16 n1, 1024 + 16 n5)
+//   h2, h3: the same on w >> 8 (n2, n6 and n3, n7).
+// v_fma_mix_f32 widens the selected f16 half exactly and computes
+//   (1024 + n) s - 1032 s = (n - 8) s   or   (1024 + 16 n) (s / 16) - 72 s = (n - 8) s
+// in one rounding of an exact result (both are integer multiples of s with at most
+// 12 significant bits), and v_cvt_pk_bf16_f32 rounds pairs to bf16 (RNE):
+// dequantW4's rounding.  Exact for 2^-122 <= |s| < 2^117 (s / 16 stays normal, and
+// 1039 |s| stays finite) and s = +-0; 17 VALU instructions per 8 weights, 12 of them
+// at half rate, against 19 (12 at half rate) for dequant8.
+struct MixScale {
+  float s, c1, s16, c2;  // s, -1032 s, s / 16, -72 s
+};
+__device__ __forceinline__ MixScale mix_scale(uint32_t sbits) {
+  const float s = __uint_as_float(sbits << 16);
+  return MixScale{s, -1032.0f * s, s * 0.0625f, -72.0f * s};
+}
+// (a & m) | o as one full-rate v_bitop3_b32 (the compiler would emit an and + an or
+// with literals, or the half-rate v_and_or_b32); m and o come in VGPRs.
+__device__ __forceinline__ uint32_t and_or(uint32_t a, uint32_t m, uint32_t o) {
+  uint32_t r;
+  asm("v_bitop3_b32 %0, %1, %2, %3 bitop3:0xea" : "=v"(r) : "v"(a), "v"(m), "v"(o));
+  return r;
+}
+__device__ __forceinline__ uint32_t pack_bf16x2(float lo, float hi) {
+  typedef float f2 __attribute__((ext_vector_type(2)));
+  typedef __bf16 b2 __attribute__((ext_vector_type(2)));
+  const f2 v = {lo, hi};
+  return __builtin_bit_cast(uint32_t, __builtin_convertvector(v, b2));
+}
+struct MixMasks {
+  uint32_t m0, m1, o;  // 0x000F000F, 0x00F000F0, 0x64006400, held in VGPRs
+};
+__device__ __forceinline__ MixMasks mix_masks() {
+  MixMasks k{0x000F000Fu, 0x00F000F0u, 0x64006400u};
+  asm volatile("" : "+v"(k.m0), "+v"(k.m1), "+v"(k.o));
+  return k;
+}
+__device__ __forceinline__ bf16x8 dequant8_mix(uint32_t w, const MixScale& S, const MixMasks& k) {
+  typedef _Float16 h2 __attribute__((ext_vector_type(2)));
+  const uint32_t w8 = w >> 8;
+  const h2 h0 = __builtin_bit_cast(h2, and_or(w, k.m0, k.o));
+  const h2 h1 = __builtin_bit_cast(h2, and_or(w, k.m1, k.o));
+  const h2 h2v = __builtin_bit_cast(h2, and_or(w8, k.m0, k.o));
+  const h2 h3 = __builtin_bit_cast(h2, and_or(w8, k.m1, k.o));
+  const float q0 = __builtin_fmaf((float)h0.x, S.s, S.c1), q4 = __builtin_fmaf((float)h0.y, S.s, S.c1);
+  const float q1 = __builtin_fmaf((float)h1.x, S.s16, S.c2), q5 = __builtin_fmaf((float)h1.y, S.s16, S.c2);
+  const float q2 = __builtin_fmaf((float)h2v.x, S.s, S.c1), q6 = __builtin_fmaf((float)h2v.y, S.s, S.c1);
+  const float q3 = __builtin_fmaf((float)h3.x, S.s16, S.c2), q7 = __builtin_fmaf((float)h3.y, S.s16, S.c2);
+  u32x4 r;
+  r[0] = pack_bf16x2(q0, q1);
+  r[1] = pack_bf16x2(q2, q3);
+  r[2] = pack_bf16x2(q4, q5);
+  r[3] = pack_bf16x2(q6, q7);
+  return __builtin_bit_cast(bf16x8, r);
+}
+
 // ================================================================ unpack
 // Flat over words: word i -> q[8i .. 8i+7].  Main part in 4-word chunks.
 __global__ void __launch_bounds__(256) unpack_kernel(const uint32_t* __restrict__ pk,
@@ -415,14 +475,34 @@ struct GroupSel {
   int N;
   int tile0;
 };
+// Branch-free, so that every kernel argument arrives in one batch of scalar loads
+// (a branch here puts the group's arguments behind a second round trip, which
+// delays the first weight load of every wave): every candidate is read and pinned
+// in SGPRs first, then the tile's matrix is picked with scalar selects.
 __device__ __forceinline__ GroupSel group_select(const GemvArgs& a, int t) {
-  GroupSel g{a.pk, a.sc, a.y, a.N, 0};
-  if (a.nmat > 1) {
-    g = GroupSel{a.gpk[0], a.gsc[0], a.gy[0], a.gN[0], a.tile0[0]};
-    if (a.nmat > 1 && t >= a.tile0[1]) g = GroupSel{a.gpk[1], a.gsc[1], a.gy[1], a.gN[1], a.tile0[1]};
-    if (a.nmat > 2 && t >= a.tile0[2]) g = GroupSel{a.gpk[2], a.gsc[2], a.gy[2], a.gN[2], a.tile0[2]};
-    if (a.nmat > 3 && t >= a.tile0[3]) g = GroupSel{a.gpk[3], a.gsc[3], a.gy[3], a.gN[3], a.tile0[3]};
+  uint64_t p[4], q[4], y[4];
+  int n[4], t0[4];
+#pragma unroll
+  for (int k = 0; k < 4; ++k) {
+    p[k] = reinterpret_cast<uint64_t>(a.gpk[k]);
+    q[k] = reinterpret_cast<uint64_t>(a.gsc[k]);
+    y[k] = reinterpret_cast<uint64_t>(a.gy[k]);
+    n[k] = a.gN[k];
+    t0[k] = a.tile0[k];
+    asm volatile("" : "+s"(p[k]), "+s"(q[k]), "+s"(y[k]), "+s"(n[k]), "+s"(t0[k]));
   }
+  uint64_t p1 = reinterpret_cast<uint64_t>(a.pk), q1 = reinterpret_cast<uint64_t>(a.sc),
+           y1 = reinterpret_cast<uint64_t>(a.y);
+  int n1 = a.N, nm = a.nmat;
+  asm volatile("" : "+s"(p1), "+s"(q1), "+s"(y1), "+s"(n1), "+s"(nm));
+  const int j = (nm > 1 && t >= t0[1]) + (nm > 2 && t >= t0[2]) + (nm > 3 && t >= t0[3]);
+  const bool grp = nm > 1;
+  GroupSel g;
+  g.pk = reinterpret_cast<const uint32_t*>(grp ? (j == 0 ? p[0] : j == 1 ? p[1] : j == 2 ? p[2] : p[3]) : p1);
+  g.sc = reinterpret_cast<const uint16_t*>(grp ? (j == 0 ? q[0] : j == 1 ? q[1] : j == 2 ? q[2] : q[3]) : q1);
+  g.y = reinterpret_cast<void*>(grp ? (j == 0 ? y[0] : j == 1 ? y[1] : j == 2 ? y[2] : y[3]) : y1);
+  g.N = grp ? (j == 0 ? n[0] : j == 1 ? n[1] : j == 2 ? n[2] : n[3]) : n1;
+  g.tile0 = grp ? (j == 0 ? t0[0] : j == 1 ? t0[1] : j == 2 ? t0[2] : t0[3]) : 0;
   return g;
 }
 
@@ -545,20 +625,28 @@ __global__ void __launch_bounds__(1024) gemv_kernel(GemvArgs a) {
 
 // ---------------------------------------------------------------- GEMV, straight-line variant
 // Same tiling as gemv_kernel, for shapes where K is a multiple of GSTEP and
-// every wave gets exactly NST steps (compile time).  A workgroup covers TPW
-// tiles of 16 rows (TPW * 16 consecutive rows), so that a whole grid fits in
-// one round of resident waves.  All loads are issued unconditionally in a
-// fixed order -- this thread's share of x first (XPT vectors, indices clamped
-// so duplicates rewrite the same LDS slot), then the NST steps of weights and
-// scales of every tile -- so the compiler's wait-count analysis is exact: x is
-// written to LDS as soon as it lands while the weights are still in flight,
-// and each step waits only for its own loads.  (vmcnt is an in-order per-wave
-// counter: a conditional load makes every later wait fall back to "all loads
-// done".)  Tiles past N (odd tile counts) recompute the last tile and are not
-// written.
+// every wave gets exactly NST steps (compile time).  A workgroup covers one
+// 16-row tile; its W = K / (GSTEP * NST) waves split K.
+//
+// Every load is issued up front, unconditionally (indices clamped) and in a fixed
+// order held by scheduling barriers: this thread's x vectors, then the scales of
+// the wave's NST steps, then its weights step by step.  vmcnt is an in-order
+// per-wave counter, so each step then waits only for its own loads, and x is
+// written to LDS as soon as it lands while the weights are still in flight.  Each
+// lane reads a step's weights and scales at constant offsets from one row pointer
+// (no per-load address arithmetic, so no address registers crowd out the data).
+// XW: each wave stages only its own K range of x (NT planes x M rows x NST * 256
+// columns, XPT vectors per lane) and reads nothing else, so it starts computing
+// without waiting for the other waves; otherwise the workgroup stages all of x
+// (XPT vectors per thread) behind one barrier.
+// Weights are expanded with dequant8_mix.  Tiles past N (odd tile counts) are
+// not written.
 // MR: rows of x the epilogue covers, 4 (M <= 4) or 16 (M <= 16; the MFMA's A
 // operand holds 16 rows of x either way, rows past M repeat row M-1).
-template <int NT, int NST, int XPT, int TPW, bool G32, int MR = 4>
+// PLAIN: one matrix, no gate/up pair (a.pk, a.sc, a.y, a.N only): the kernel then
+// reads none of the group or pair arguments, whose selection the compiler turns into
+// branches with late scalar loads that delay every wave's first weight load.
+template <int NT, int NST, int XPT, bool G32, int MR, bool XW, bool PLAIN = false>
 __global__ void __launch_bounds__(1024) gemv_fast_kernel(GemvArgs a) {
   extern __shared__ __attribute__((aligned(16))) uint16_t lds[];
   const int lane = threadIdx.x & 63;
@@ -567,107 +655,123 @@ __global__ void __launch_bounds__(1024) gemv_fast_kernel(GemvArgs a) {
   const int r = lane & 15;
   const int c = lane >> 4;
   const int s0 = wave * NST;
-  // the block's matrix (a weight group's member, or the single weight) and its first tile
-  const GroupSel gs = group_select(a, (int)blockIdx.x * TPW);
+  // the block's matrix (a weight group's member, or the single weight) and its tile
+  const GroupSel gs = PLAIN ? GroupSel{a.pk, a.sc, a.y, a.N, 0} : group_select(a, (int)blockIdx.x);
+  const int pair_f = PLAIN ? 0 : a.pair_f;
   const int N = gs.N;
-  const int bt = (int)blockIdx.x * TPW - gs.tile0;
-  const int ntiles = (N + 15) >> 4;
+  const int bt = (int)blockIdx.x - gs.tile0;
+  const int K = a.K;
+  const int plane = a.M * K;
 
-  // 1. x loads (this thread's share), unconditional
-  const int nvec = (NT * a.M * a.K) >> 3;
-  const uint4* xsrc = reinterpret_cast<const uint4*>(a.x);
-  uint4 xv[XPT];
+  // 1. x loads, first (they need nothing but x's address)
+  typedef __attribute__((address_space(1))) const u32x4 g_u4;
+  typedef __attribute__((address_space(1))) const uint32_t g_u32;
+  const u32x4* xsrc = reinterpret_cast<const u32x4*>(a.x);
   int xi[XPT];
+  if (XW) {
+    // vector v of the wave's share: (plane t, row m) = v / (NST * 32), column vector
+    // s0 * 32 + v % (NST * 32) of that row
+    const int nv = NT * a.M * NST * 32;
 #pragma unroll
-  for (int i = 0; i < XPT; ++i) {
-    xi[i] = min((int)threadIdx.x + i * (int)blockDim.x, nvec - 1);
-    xv[i] = xsrc[xi[i]];
+    for (int i = 0; i < XPT; ++i) {
+      const int v = min(lane + 64 * i, nv - 1);
+      xi[i] = (v / (NST * 32)) * (K >> 3) + s0 * 32 + v % (NST * 32);
+    }
+  } else {
+    const int nvec = (NT * plane) >> 3;
+#pragma unroll
+    for (int i = 0; i < XPT; ++i) xi[i] = min((int)threadIdx.x + i * (int)blockDim.x, nvec - 1);
   }
-
-  // 2. weight and scale loads of this wave's NST steps of every tile, unconditional
-  uint4 wv[TPW][NST][VPL];
-  uint32_t sv[TPW][NST];
+  u32x4 xv[XPT];
 #pragma unroll
-  for (int tp = 0; tp < TPW; ++tp) {
-    const int tile = min(bt + tp, ntiles - 1);
-    const uint32_t* pkrow;
-    const uint16_t* scrow;
-    weight_row(gs.pk, gs.sc, a.pk2, a.sc2, a.pair_f, tile * 16 + r, N, a.K, a.groups_per_row, pkrow, scrow);
+  for (int i = 0; i < XPT; ++i) xv[i] = xsrc[xi[i]];
+  __builtin_amdgcn_sched_barrier(0);
+
+  // row pointers (pinned in VGPRs as global-memory pointers, so that the compiler
+  // forms no address between the loads below)
+  const int tile = min(bt, ((N + 15) >> 4) - 1);
+  const uint32_t* pkrow;
+  const uint16_t* scrow;
+  weight_row(gs.pk, gs.sc, a.pk2, a.sc2, pair_f, tile * 16 + r, N, K, a.groups_per_row, pkrow, scrow);
+  g_u4* wb = (g_u4*)(reinterpret_cast<const u32x4*>(pkrow) + s0 * 8 + c * 2);
+  g_u32* sb = (g_u32*)(reinterpret_cast<const uint32_t*>(scrow) + s0 * 4 + c);
+  asm volatile("" : "+v"(wb), "+v"(sb));
+  __builtin_amdgcn_sched_barrier(0);
+
+  // 2. scales, then 3. weights, of this wave's NST steps
+  uint32_t sv[NST];  // two bf16 scales (low half: the step's first vector)
+  if (G32) {
+#pragma unroll
+    for (int i = 0; i < NST; ++i) sv[i] = sb[4 * i];
+  } else {
 #pragma unroll
     for (int i = 0; i < NST; ++i) {
       const int g0 = ((s0 + i) * 4 + c) * VPL;
-#pragma unroll
-      for (int v = 0; v < VPL; ++v) wv[tp][i][v] = *reinterpret_cast<const uint4*>(pkrow + 4 * (g0 + v));
-      if (G32) {
-        sv[tp][i] = *reinterpret_cast<const uint32_t*>(scrow + g0);
-      } else {
-        sv[tp][i] = (uint32_t)scrow[g0 / a.group_chunks] | ((uint32_t)scrow[(g0 + 1) / a.group_chunks] << 16);
-      }
+      sv[i] = (uint32_t)scrow[g0 / a.group_chunks] | ((uint32_t)scrow[(g0 + 1) / a.group_chunks] << 16);
     }
   }
+  __builtin_amdgcn_sched_barrier(0);
+  u32x4 wv[NST][VPL];
+#pragma unroll
+  for (int i = 0; i < NST; ++i) {
+    wv[i][0] = wb[8 * i];
+    wv[i][1] = wb[8 * i + 1];
+  }
+  __builtin_amdgcn_sched_barrier(0);
 
-  // 3. x -> LDS, barrier
-  uint4* xdst = reinterpret_cast<uint4*>(lds);
+  // 4. x -> LDS ([NT][M][K] halves); with XW a wave reads only what it wrote, and a
+  // wave's LDS accesses complete in order, so no barrier is needed
+  u32x4* xdst = reinterpret_cast<u32x4*>(lds);
 #pragma unroll
   for (int i = 0; i < XPT; ++i) xdst[xi[i]] = xv[i];
-  __syncthreads();
+  if (!XW) __syncthreads();
 
-  uint32_t kM = 0x000F000Fu, kO = 0x43004300u;
-  asm volatile("" : "+v"(kM), "+v"(kO));
-  floatx4 acc[TPW];
-  const int plane = a.M * a.K;
-  const uint16_t* xrow = lds + min(r, a.M - 1) * a.K;
+  const MixMasks km = mix_masks();
+  floatx4 acc = {0.f, 0.f, 0.f, 0.f};
+  const uint16_t* xrow = lds + min(r, a.M - 1) * K;
 #pragma unroll
-  for (int tp = 0; tp < TPW; ++tp) {
-    acc[tp] = floatx4{0.f, 0.f, 0.f, 0.f};
+  for (int i = 0; i < NST; ++i) {
 #pragma unroll
-    for (int i = 0; i < NST; ++i) {
+    for (int v = 0; v < VPL; ++v) {
+      const int g = ((s0 + i) * 4 + c) * VPL + v;
+      const MixScale S = mix_scale(v == 0 ? (sv[i] & 0xffffu) : (sv[i] >> 16));
+      const uint16_t* xr = xrow + 32 * g;
+      const uint32_t wj[4] = {wv[i][v][0], wv[i][v][1], wv[i][v][2], wv[i][v][3]};
 #pragma unroll
-      for (int v = 0; v < VPL; ++v) {
-        const int g = ((s0 + i) * 4 + c) * VPL + v;
-        const uint32_t slo = v == 0 ? (sv[tp][i] & 0xffffu) : (sv[tp][i] >> 16);
-        const uint32_t shi = slo << 16;
-        const float cneg = -136.0f * __uint_as_float(shi);
-        const uint16_t* xr = xrow + 32 * g;
-        const uint32_t wj[4] = {wv[tp][i][v].x, wv[tp][i][v].y, wv[tp][i][v].z, wv[tp][i][v].w};
+      for (int j = 0; j < 4; ++j) {
+        const bf16x8 bb = dequant8_mix(wj[j], S, km);
 #pragma unroll
-        for (int j = 0; j < 4; ++j) {
-          const bf16x8 bb = dequant8(wj[j], slo, shi, cneg, kM, kO);
-#pragma unroll
-          for (int t = 0; t < NT; ++t)
-            mfma_acc(acc[tp], *reinterpret_cast<const bf16x8*>(xr + t * plane + 8 * j), bb);
-        }
+        for (int t = 0; t < NT; ++t)
+          acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(*reinterpret_cast<const bf16x8*>(xr + t * plane + 8 * j), bb,
+                                                        acc, 0, 0, 0);
       }
     }
   }
-  mfma_drain<TPW>(acc);
 
   // D: lane (r, c) holds rows m = 4c + i of column r; MR = 4 keeps c == 0 only
-  float* red = reinterpret_cast<float*>(lds + NT * plane);  // [TPW][waves][MR][16]
+  float* red = reinterpret_cast<float*>(lds + NT * plane);  // [waves][MR][16]
   if (MR == 16 || c == 0) {
 #pragma unroll
-    for (int tp = 0; tp < TPW; ++tp)
-#pragma unroll
-      for (int i = 0; i < 4; ++i) red[((tp * nwaves + wave) * MR + (MR == 16 ? 4 * c : 0) + i) * 16 + r] = acc[tp][i];
+    for (int i = 0; i < 4; ++i) red[(wave * MR + (MR == 16 ? 4 * c : 0) + i) * 16 + r] = acc[i];
   }
   __syncthreads();
-  for (int t = (int)threadIdx.x; t < 16 * MR * TPW; t += (int)blockDim.x) {
-    const int tp = t / (16 * MR), m = (t >> 4) % MR, rr = t & 15;
-    const int n = (bt + tp) * 16 + rr;
-    if (a.pair_f) {
+  for (int t = (int)threadIdx.x; t < 16 * MR; t += (int)blockDim.x) {
+    const int m = t >> 4, rr = t & 15;
+    const int n = bt * 16 + rr;
+    if (pair_f) {
       // gate row rr < 8 of the tile and its up row rr + 8
-      const int f = ((bt + tp) << 3) + rr;
-      if (rr < 8 && m < a.M && f < a.pair_f) {
+      const int f = (bt << 3) + rr;
+      if (rr < 8 && m < a.M && f < pair_f) {
         float g = 0.f, u = 0.f;
         for (int w = 0; w < nwaves; ++w) {
-          g += red[((tp * nwaves + w) * MR + m) * 16 + rr];
-          u += red[((tp * nwaves + w) * MR + m) * 16 + rr + 8];
+          g += red[(w * MR + m) * 16 + rr];
+          u += red[(w * MR + m) * 16 + rr + 8];
         }
-        store_gelu_mul(a.y, a.y_f32, a.bf16_dots, (int64_t)m * a.pair_f + f, g, u);
+        store_gelu_mul(a.y, a.y_f32, a.bf16_dots, (int64_t)m * pair_f + f, g, u);
       }
     } else if (m < a.M && n < N) {
       float v = 0.f;
-      for (int w = 0; w < nwaves; ++w) v += red[((tp * nwaves + w) * MR + m) * 16 + rr];
+      for (int w = 0; w < nwaves; ++w) v += red[(w * MR + m) * 16 + rr];
       if (a.y_f32) reinterpret_cast<float*>(gs.y)[(int64_t)m * N + n] = v;
       else reinterpret_cast<uint16_t*>(gs.y)[(int64_t)m * N + n] = (uint16_t)f32_to_bf16_rne(v);
     }
@@ -1486,7 +1590,78 @@ hipError_t w4l_fill_zero(void* p, int64_t bytes, hipStream_t st) {
 }
 
 
-bool w4l_gemv16_plan(int64_t M, int64_t N, int64_t K, int nterms, int* nst_out, int* waves_out, int* xpt_out);
+// ---------------------------------------------------------------- decode GEMV plans
+namespace {
+struct GemvPlan {
+  int nst;    // steps of GSTEP columns per wave
+  int waves;  // waves per workgroup, K / (GSTEP * nst)
+  int xpt;    // x vectors per lane (per-wave staging) or per thread (workgroup staging)
+  bool xw;    // each wave stages only its own K range of x
+};
+// About ten resident waves per SIMD on 256 CUs: a grid of at most this many waves
+// issues every load in its first round.
+constexpr int64_t GEMV_ONE_ROUND_WAVES = 10240;
+
+int pow2_at_least(int64_t v) {
+  int p = 1;
+  while (p < v) p *= 2;
+  return p;
+}
+
+// Straight-line GEMV plan for the 4-row (mr = 4, M <= 4) or 16-row (mr = 16,
+// 4 < M <= 16, bf16 x) epilogue.  Per-wave x staging when a wave's share of x,
+// nterms * M * nst * 256 columns, takes at most 8 vectors per lane; then the fewest
+// steps per wave (the most waves, up to 16 per workgroup) whose grid of
+// tiles * waves stays within one round, else the fewest waves.  Measured (us, 12B
+// rows at M = 1, against the next choice): gate/up 1920 tiles, nst 3 15.0 against
+// nst 1 17.4 and nst 5 15.4; down (K = 15360) nst 4 9.6 against nst 5 9.9 and 6
+// 10.7; q, k/v, o nst 1 4.3 / 4.1 / 4.3 against nst 3 (2 for o) 5.1 / 4.9 / 4.6; E2B
+// down nst 2 5.1 against 3 5.3; full-layer o (K = 8192) nst 2 6.8 against 4 7.4.
+// Otherwise (f32 x or 16 rows beyond that share) the workgroup stages all of x behind
+// a barrier: the first nst of {5, 2, 4, 1, 3, 6} (4-row form) or the smallest of 1..6
+// (16-row form) with at most 16 waves and 8 vectors per thread.
+bool gemv_plan(int64_t M, int64_t N, int64_t K, int nterms, int mr, GemvPlan* out) {
+  if (K % w4k::GSTEP != 0 || M < 1 || N <= 0 || K > (1 << 20)) return false;
+  if (mr == 4 ? M > 4 : (M > 16 || nterms != 1)) return false;
+  const int64_t steps = K / w4k::GSTEP, tiles = (N + 15) / 16;
+  const int64_t lds_x = (int64_t)nterms * M * K * 2;
+  static const int cand[] = {1, 2, 3, 4, 5, 6, 8};
+  bool have = false;
+  GemvPlan best{};
+  for (int nst : cand) {
+    if (steps % nst != 0 || steps / nst > 16) continue;
+    if (nterms == 3 && nst > 5) continue;  // the f32-x instances
+    if (mr == 16 && nst != 1) continue;    // the 16-row per-wave instances
+    const int64_t nv = (int64_t)nterms * M * nst * 32;
+    if (nv > 64 * 8) continue;
+    const int waves = (int)(steps / nst);
+    if (lds_x + (int64_t)waves * mr * 16 * 4 > 160 * 1024) continue;
+    best = GemvPlan{nst, waves, pow2_at_least((nv + 63) / 64), true};
+    have = true;
+    if (tiles * waves <= GEMV_ONE_ROUND_WAVES) break;
+  }
+  if (have) {
+    *out = best;
+    return true;
+  }
+  if (nterms == 1 && mr == 4) return false;  // callers take the 16-row or skinny route
+  static const int pref4[] = {5, 2, 4, 1, 3, 6};
+  static const int pref16[] = {1, 2, 3, 4, 5, 6};
+  for (int k = 0; k < 6; ++k) {
+    const int nst = mr == 4 ? pref4[k] : pref16[k];
+    if (steps % nst != 0 || steps / nst > 16) continue;
+    const int waves = (int)(steps / nst);
+    const int64_t nvec = (int64_t)nterms * M * K / 8;
+    const int64_t per = (nvec + 64 * waves - 1) / (64 * waves);
+    if (per > 8) continue;
+    if (lds_x + (int64_t)waves * mr * 16 * 4 > 160 * 1024) continue;
+    *out = GemvPlan{nst, waves, pow2_at_least(per), false};
+    return true;
+  }
+  return false;
+}
+}  // namespace
+
 // M <= 16 through the 16-row GEMV (for M <= 4 where the 4-row plan does not
 // hold) when its plan holds and every 16-row tile
 // re-reading x from L2 stays under 40 MiB:
@@ -1494,14 +1669,19 @@ bool w4l_gemv16_plan(int64_t M, int64_t N, int64_t K, int nterms, int* nst_out, 
 // E2B) and the skinny kernel, whose workgroups share x over 64-128 rows, wins
 // above it (12B gate/up, full-layer q at M = 16).
 bool w4l_gemv16_ok(int64_t M, int64_t N, int64_t K, int nterms) {
-  int nst, waves, xpt;
-  if (!w4l_gemv16_plan(M, N, K, nterms, &nst, &waves, &xpt)) return false;
+  GemvPlan p;
+  if (!gemv_plan(M, N, K, nterms, 16, &p)) return false;
   const int64_t max_bytes = 40ll << 20;
   return (N + 15) / 16 * M * K * 2 <= max_bytes;
 }
 
 bool w4l_gemv_ok(int64_t M, int64_t K, int nterms) {
   return M >= 1 && M <= 4 && (int64_t)nterms * M * K * 2 + 16 * 4 * 16 * 4 <= 65536;
+}
+
+bool w4l_gemv_fast_ok(int64_t M, int64_t N, int64_t K, int nterms) {
+  GemvPlan p;
+  return w4l_gemv_ok(M, K, nterms) && gemv_plan(M, N, K, nterms, 4, &p);
 }
 
 int w4l_gemv_waves(int64_t N, int64_t K) {
@@ -1513,62 +1693,6 @@ int w4l_gemv_waves(int64_t N, int64_t K) {
   return (int)w;
 }
 
-// Straight-line GEMV plan: steps per wave NST (exact divisor of the step
-// count, in the order below) and x vectors per thread XPT (power of two <= 8).
-bool w4l_gemv_fast_plan(int64_t M, int64_t N, int64_t K, int nterms, int* nst_out, int* waves_out,
-                        int* xpt_out, int* tpw_out) {
-  if (K % w4k::GSTEP != 0) return false;
-  const int64_t steps = K / w4k::GSTEP;
-  // measured order on the 12B / 1B decode shapes (K = 1536..15360): five steps per
-  // wave streams best when it divides K/256, then two, four, one
-  static const int pref[] = {5, 2, 4, 1, 3, 6};
-  int nst = 0, waves = 0;
-  for (int p : pref) {
-    if (nst) break;
-    if (steps % p == 0 && steps / p <= 16) { nst = p; waves = (int)(steps / p); break; }
-  }
-  if (!nst) return false;
-  // one 16-row tile per workgroup (two measured slower on every decode shape)
-  const int tpw = 1;
-  const int64_t nvec = (int64_t)nterms * M * K / 8;
-  const int64_t per = (nvec + 64 * waves - 1) / (64 * waves);
-  int xpt = 1;
-  while (xpt < per) xpt *= 2;
-  if (xpt > 8) return false;
-  *nst_out = nst;
-  *waves_out = waves;
-  *xpt_out = xpt;
-  *tpw_out = tpw;
-  return true;
-}
-
-// Straight-line GEMV for 4 < M <= 16 (bf16 x): the same kernel with a 16-row
-// epilogue.  As many waves as K / 256 allows (<= 16) so that each thread stages
-// at most 8 x vectors; x [M][K] sits in LDS whole (up to 160 KB on gfx950).
-bool w4l_gemv16_plan(int64_t M, int64_t N, int64_t K, int nterms, int* nst_out, int* waves_out, int* xpt_out) {
-  if (nterms != 1 || M < 1 || M > 16 || K % w4k::GSTEP != 0 || N <= 0) return false;
-  const int64_t steps = K / w4k::GSTEP;
-  int nst = 0;
-  for (int p = 1; p <= 6 && !nst; ++p)
-    if (steps % p == 0 && steps / p <= 16) nst = p;
-  if (!nst) return false;
-  const int waves = (int)(steps / nst);
-  const int64_t nvec = M * K / 8;
-  const int64_t per = (nvec + 64 * waves - 1) / (64 * waves);
-  int xpt = 1;
-  while (xpt < per) xpt *= 2;
-  if (xpt > 8) return false;
-  const int64_t lds = M * K * 2 + (int64_t)waves * 16 * 16 * 4;
-  if (lds > 160 * 1024) return false;
-  *nst_out = nst;
-  *waves_out = waves;
-  *xpt_out = xpt;
-  return true;
-}
-
-// Launch of gemv_fast_kernel for a filled GemvArgs: the template arguments
-// follow the plan (x planes, steps per wave, x vectors per thread, tiles per
-// workgroup, group 32).
 // LDS above 64 KB per workgroup needs the kernel's attribute raised once.
 template <class Kern>
 static hipError_t allow_big_lds(Kern k, size_t lds) {
@@ -1577,139 +1701,89 @@ static hipError_t allow_big_lds(Kern k, size_t lds) {
                              160 * 1024);
 }
 
-// M <= 16 form (mr = 16, bf16 x, one tile per workgroup): nst 1..2, xpt 1..8.
-static hipError_t gemv16_launch(const w4k::GemvArgs& a, int nst, int waves, int xpt, int nblocks, bool g32,
+template <int NT, int NST, int XPT, int MR, bool XW>
+static hipError_t gemv_fast_one(const w4k::GemvArgs& a, dim3 grid, dim3 block, size_t lds, bool g32,
                                 hipStream_t st) {
-  const size_t lds = (size_t)a.M * a.K * 2 + (size_t)waves * 16 * 16 * 4;
-  const dim3 grid((unsigned)nblocks), block(64 * waves);
-  hipError_t e = hipSuccess;
-#define W4_G16(NST_, XPT_)                                                                  \
-  do {                                                                                      \
-    if (g32) {                                                                              \
-      auto k = w4k::gemv_fast_kernel<1, NST_, XPT_, 1, true, 16>;                           \
-      if ((e = allow_big_lds(k, lds)) != hipSuccess) return e;                              \
-      hipLaunchKernelGGL(k, grid, block, lds, st, a);                                       \
-    } else {                                                                                \
-      auto k = w4k::gemv_fast_kernel<1, NST_, XPT_, 1, false, 16>;                          \
-      if ((e = allow_big_lds(k, lds)) != hipSuccess) return e;                              \
-      hipLaunchKernelGGL(k, grid, block, lds, st, a);                                       \
-    }                                                                                       \
-  } while (0)
-#define W4_G16_X(NST_)                      \
-  switch (xpt) {                            \
-    case 1: W4_G16(NST_, 1); break;         \
-    case 2: W4_G16(NST_, 2); break;         \
-    case 4: W4_G16(NST_, 4); break;         \
-    default: W4_G16(NST_, 8); break;        \
-  }
-  switch (nst) {
-    case 1: W4_G16_X(1); break;
-    case 2: W4_G16_X(2); break;
-    case 3: W4_G16_X(3); break;
-    case 4: W4_G16_X(4); break;
-    case 5: W4_G16_X(5); break;
-    default: W4_G16_X(6); break;
-  }
-#undef W4_G16_X
-#undef W4_G16
+  // the plain single-matrix form for bf16 x with per-wave staging and the 4-row epilogue
+  const bool plain = NT == 1 && MR == 4 && XW && a.nmat <= 1 && a.pair_f == 0;
+  auto k = plain ? (g32 ? w4k::gemv_fast_kernel<NT, NST, XPT, true, MR, XW, NT == 1 && MR == 4 && XW>
+                        : w4k::gemv_fast_kernel<NT, NST, XPT, false, MR, XW, NT == 1 && MR == 4 && XW>)
+                 : (g32 ? w4k::gemv_fast_kernel<NT, NST, XPT, true, MR, XW> : w4k::gemv_fast_kernel<NT, NST, XPT, false, MR, XW>);
+  hipError_t e = allow_big_lds(k, lds);
+  if (e != hipSuccess) return e;
+  hipLaunchKernelGGL(k, grid, block, lds, st, a);
   return hipGetLastError();
 }
 
-static hipError_t gemv_fast_launch(const w4k::GemvArgs& a, int nterms, int nst, int waves, int xpt, int tpw,
-                                   int nblocks, bool g32, hipStream_t st) {
-  const size_t lds = (size_t)nterms * a.M * a.K * 2 + (size_t)tpw * waves * 4 * 16 * 4;
-  const dim3 grid((unsigned)nblocks), block(64 * waves);
-#define W4_FAST(NT_, NST_, XPT_, TPW_)                                                                          \
-  do {                                                                                                          \
-    if (g32) hipLaunchKernelGGL((w4k::gemv_fast_kernel<NT_, NST_, XPT_, TPW_, true>), grid, block, lds, st, a); \
-    else hipLaunchKernelGGL((w4k::gemv_fast_kernel<NT_, NST_, XPT_, TPW_, false>), grid, block, lds, st, a);    \
-  } while (0)
-#define W4_FAST_T(NT_, NST_, XPT_) W4_FAST(NT_, NST_, XPT_, 1)
-#define W4_FAST_X(NT_, NST_)                    \
-  switch (xpt) {                                \
-    case 1: W4_FAST_T(NT_, NST_, 1); break;     \
-    case 2: W4_FAST_T(NT_, NST_, 2); break;     \
-    case 4: W4_FAST_T(NT_, NST_, 4); break;     \
-    default: W4_FAST_T(NT_, NST_, 8); break;    \
+// Launch of gemv_fast_kernel for a filled GemvArgs and a plan (instances: bf16 x with
+// per-wave staging, steps 1..6 and 8; f32 x per wave up to 5 steps, or the workgroup
+// form; the 16-row epilogue per wave at 1 step, or the workgroup form).
+static hipError_t gemv_fast_launch(const w4k::GemvArgs& a, int nterms, int mr, const GemvPlan& p, int nblocks,
+                                   bool g32, hipStream_t st) {
+  const size_t lds = (size_t)nterms * a.M * a.K * 2 + (size_t)p.waves * mr * 16 * 4;
+  const dim3 grid((unsigned)nblocks), block(64 * p.waves);
+#define W4_GF(NT_, NST_, MR_, XW_)                                                          \
+  switch (p.xpt) {                                                                          \
+    case 1: return gemv_fast_one<NT_, NST_, 1, MR_, XW_>(a, grid, block, lds, g32, st);     \
+    case 2: return gemv_fast_one<NT_, NST_, 2, MR_, XW_>(a, grid, block, lds, g32, st);     \
+    case 4: return gemv_fast_one<NT_, NST_, 4, MR_, XW_>(a, grid, block, lds, g32, st);     \
+    case 8: return gemv_fast_one<NT_, NST_, 8, MR_, XW_>(a, grid, block, lds, g32, st);     \
+    default: return hipErrorInvalidValue;                                                   \
   }
-#define W4_FAST_N(NT_)                         \
-  switch (nst) {                               \
-    case 1: W4_FAST_X(NT_, 1); break;          \
-    case 2: W4_FAST_X(NT_, 2); break;          \
-    case 3: W4_FAST_X(NT_, 3); break;          \
-    case 4: W4_FAST_X(NT_, 4); break;          \
-    case 5: W4_FAST_X(NT_, 5); break;          \
-    default: W4_FAST_X(NT_, 6); break;         \
+#define W4_GF6(NT_, MR_, XW_)                     \
+  switch (p.nst) {                                \
+    case 1: W4_GF(NT_, 1, MR_, XW_)               \
+    case 2: W4_GF(NT_, 2, MR_, XW_)               \
+    case 3: W4_GF(NT_, 3, MR_, XW_)               \
+    case 4: W4_GF(NT_, 4, MR_, XW_)               \
+    case 5: W4_GF(NT_, 5, MR_, XW_)               \
+    case 6: W4_GF(NT_, 6, MR_, XW_)               \
+    default: return hipErrorInvalidValue;         \
   }
-  if (nterms == 1) { W4_FAST_N(1) } else { W4_FAST_N(3) }
-#undef W4_FAST_N
-#undef W4_FAST_X
-#undef W4_FAST_T
-#undef W4_FAST
-  return hipGetLastError();
+  if (mr == 4 && nterms == 1 && p.xw) {
+    switch (p.nst) {
+      case 1: W4_GF(1, 1, 4, true)
+      case 2: W4_GF(1, 2, 4, true)
+      case 3: W4_GF(1, 3, 4, true)
+      case 4: W4_GF(1, 4, 4, true)
+      case 5: W4_GF(1, 5, 4, true)
+      case 6: W4_GF(1, 6, 4, true)
+      case 8: W4_GF(1, 8, 4, true)
+      default: return hipErrorInvalidValue;
+    }
+  }
+  if (mr == 4 && nterms == 3 && p.xw) {
+    switch (p.nst) {
+      case 1: W4_GF(3, 1, 4, true)
+      case 2: W4_GF(3, 2, 4, true)
+      case 3: W4_GF(3, 3, 4, true)
+      case 4: W4_GF(3, 4, 4, true)
+      case 5: W4_GF(3, 5, 4, true)
+      default: return hipErrorInvalidValue;
+    }
+  }
+  if (mr == 4 && nterms == 3) W4_GF6(3, 4, false)
+  if (mr == 16 && nterms == 1 && p.xw) {
+    if (p.nst != 1) return hipErrorInvalidValue;
+    W4_GF(1, 1, 16, true)
+  }
+  if (mr == 16 && nterms == 1) W4_GF6(1, 16, false)
+#undef W4_GF6
+#undef W4_GF
+  return hipErrorInvalidValue;
 }
 
 hipError_t w4l_gemv(const uint16_t* x_planes, int nterms, const int32_t* pk, const uint16_t* sc,
                     void* y, int y_f32, int64_t M, int64_t N, int64_t K, int32_t group,
                     hipStream_t st, const W4Pair* pair) {
   if (pair) N = 16 * ((pair->F + 7) / 8);
-  bool m16 = M > 4;
-  if (!m16 && nterms == 1) {
-    // M <= 4 beyond the 4-row form (x over its 64 KiB of LDS or 8 vectors per
-    // thread): the 16-row form
-    int a0, a1, a2, a3;
-    const bool four = w4l_gemv_ok(M, K, 1) && w4l_gemv_fast_plan(M, N, K, 1, &a0, &a1, &a2, &a3);
-    m16 = !four && w4l_gemv16_plan(M, N, K, 1, &a0, &a1, &a2);
+  // the 4-row form where its plan holds, else the 16-row form (M <= 16, bf16 x)
+  GemvPlan p;
+  int mr = 4;
+  if (!(w4l_gemv_ok(M, K, nterms) && gemv_plan(M, N, K, nterms, 4, &p))) {
+    mr = 16;
+    if (!gemv_plan(M, N, K, nterms, 16, &p)) mr = 0;
   }
-  if (m16) {
-    int nst, waves, xpt;
-    if (!w4l_gemv16_plan(M, N, K, nterms, &nst, &waves, &xpt)) return hipErrorInvalidValue;
-    w4k::GemvArgs a{};
-    a.x = x_planes;
-    a.pk = reinterpret_cast<const uint32_t*>(pk);
-    a.sc = sc;
-    a.y = y;
-    a.M = (int)M;
-    a.N = (int)N;
-    a.K = (int)K;
-    a.group_chunks = group / 32;
-    a.groups_per_row = (int)(K / group);
-    a.y_f32 = y_f32;
-    a.steps = (int)(K / w4k::GSTEP);
-    if (pair) {
-      a.pk2 = reinterpret_cast<const uint32_t*>(pair->pk_up);
-      a.sc2 = pair->sc_up;
-      a.pair_f = (int)pair->F;
-      a.bf16_dots = pair->bf16_dots;
-    }
-    return gemv16_launch(a, nst, waves, xpt, (int)((N + 15) / 16), group == 32, st);
-  }
-  {
-    int nst, waves, xpt, tpw;
-    if (w4l_gemv_fast_plan(M, N, K, nterms, &nst, &waves, &xpt, &tpw)) {
-      w4k::GemvArgs a{};
-      a.x = x_planes;
-      a.pk = reinterpret_cast<const uint32_t*>(pk);
-      a.sc = sc;
-      a.y = y;
-      a.M = (int)M;
-      a.N = (int)N;
-      a.K = (int)K;
-      a.group_chunks = group / 32;
-      a.groups_per_row = (int)(K / group);
-      a.y_f32 = y_f32;
-      a.steps = (int)(K / w4k::GSTEP);
-      if (pair) {
-        a.pk2 = reinterpret_cast<const uint32_t*>(pair->pk_up);
-        a.sc2 = pair->sc_up;
-        a.pair_f = (int)pair->F;
-        a.bf16_dots = pair->bf16_dots;
-      }
-      const int64_t tiles = (N + 15) / 16;
-      return gemv_fast_launch(a, nterms, nst, waves, xpt, tpw, (int)((tiles + tpw - 1) / tpw), group == 32, st);
-    }
-  }
-  if (pair) return hipErrorInvalidValue;
   w4k::GemvArgs a{};
   a.x = x_planes;
   a.pk = reinterpret_cast<const uint32_t*>(pk);
@@ -1721,6 +1795,17 @@ hipError_t w4l_gemv(const uint16_t* x_planes, int nterms, const int32_t* pk, con
   a.group_chunks = group / 32;
   a.groups_per_row = (int)(K / group);
   a.y_f32 = y_f32;
+  if (pair) {
+    a.pk2 = reinterpret_cast<const uint32_t*>(pair->pk_up);
+    a.sc2 = pair->sc_up;
+    a.pair_f = (int)pair->F;
+    a.bf16_dots = pair->bf16_dots;
+  }
+  if (mr) {
+    a.steps = (int)(K / w4k::GSTEP);
+    return gemv_fast_launch(a, nterms, mr, p, (int)((N + 15) / 16), group == 32, st);
+  }
+  if (pair) return hipErrorInvalidValue;
   a.steps = (int)((K + w4k::GSTEP - 1) / w4k::GSTEP);
   const int waves = w4l_gemv_waves(N, K);
   const size_t lds = (size_t)nterms * M * K * 2 + (size_t)waves * 4 * 16 * 4;
@@ -2082,11 +2167,7 @@ static bool skinny_mid(int64_t M, int64_t N, int64_t K, int nterms) {
 hipError_t w4l_linear(const uint16_t* x_planes, int nterms, const int32_t* pk, const uint16_t* sc,
                       void* y, int y_f32, int64_t M, int64_t N, int64_t K, int32_t group,
                       hipStream_t st) {
-  {
-    int a0, a1, a2, a3;
-    if (w4l_gemv_ok(M, K, nterms) && w4l_gemv_fast_plan(M, N, K, nterms, &a0, &a1, &a2, &a3))
-      return w4l_gemv(x_planes, nterms, pk, sc, y, y_f32, M, N, K, group, st);
-  }
+  if (w4l_gemv_fast_ok(M, N, K, nterms)) return w4l_gemv(x_planes, nterms, pk, sc, y, y_f32, M, N, K, group, st);
   if (w4l_gemv16_ok(M, N, K, nterms)) return w4l_gemv(x_planes, nterms, pk, sc, y, y_f32, M, N, K, group, st);
   // M <= 4 beyond both GEMV plans (12B gate/up rows at M = 4): the skinny kernel,
   // 23.5 -> 19 us against the generic GEMV below
@@ -2139,9 +2220,7 @@ enum PairRoute { PAIR_NONE, PAIR_GEMV, PAIR_PREFILL, PAIR_SKINNY };
 // kernel also takes decode shapes the straight-line GEMV plan cannot hold (its
 // x rows past M repeat row M - 1 and are not stored).
 PairRoute pair_route(int64_t M, int64_t F, int64_t K, int nterms) {
-  int nst, waves, xpt, tpw;
-  if (w4l_gemv_ok(M, K, nterms) && w4l_gemv_fast_plan(M, 16 * ((F + 7) / 8), K, nterms, &nst, &waves, &xpt, &tpw))
-    return PAIR_GEMV;
+  if (w4l_gemv_fast_ok(M, 16 * ((F + 7) / 8), K, nterms)) return PAIR_GEMV;
   if (w4l_gemv16_ok(M, 16 * ((F + 7) / 8), K, nterms)) return PAIR_GEMV;
   if (skinny_mid(M, 16 * ((F + 7) / 8), K, nterms)) return PAIR_SKINNY;
   if (w4l_prefill_ok(M, K, nterms)) return PAIR_PREFILL;
@@ -2174,22 +2253,23 @@ hipError_t w4l_gelu_mul(const float* g, const float* u, void* h, int h_f32, int 
 }
 
 bool w4l_group_fused(int64_t M, int64_t Ntot, int64_t K, int nterms) {
-  int nst, waves, xpt, tpw;
-  if (M <= 4 && w4l_gemv_ok(M, K, nterms) && w4l_gemv_fast_plan(M, 16, K, nterms, &nst, &waves, &xpt, &tpw))
-    return true;
+  if (M <= 4 && w4l_gemv_fast_ok(M, Ntot, K, nterms)) return true;
   return w4l_gemv16_ok(M, Ntot, K, nterms);
 }
 
 hipError_t w4l_gemv_group(const uint16_t* x_planes, int nterms, int n, const int32_t* const* pk,
                           const uint16_t* const* sc, void* const* y, const int64_t* N, int y_f32, int64_t M, int64_t K,
                           int32_t group, hipStream_t st) {
-  int nst, waves, xpt, tpw;
-  // the 4-row form where its plan holds, else the 16-row form (M <= 16)
-  const bool m16 = M > 4 || !w4l_gemv_ok(M, K, nterms) || !w4l_gemv_fast_plan(M, 16, K, nterms, &nst, &waves, &xpt, &tpw);
   if (n < 1 || n > 4) return hipErrorInvalidValue;
-  if (m16 ? !w4l_gemv16_plan(M, 16, K, nterms, &nst, &waves, &xpt)
-          : (!w4l_gemv_ok(M, K, nterms) || !w4l_gemv_fast_plan(M, 16, K, nterms, &nst, &waves, &xpt, &tpw)))
-    return hipErrorInvalidValue;
+  int64_t ntot = 0;
+  for (int j = 0; j < n; ++j) ntot += 16 * ((N[j] + 15) / 16);
+  // the 4-row form where its plan holds, else the 16-row form (M <= 16)
+  GemvPlan p;
+  int mr = 4;
+  if (!(w4l_gemv_ok(M, K, nterms) && gemv_plan(M, ntot, K, nterms, 4, &p))) {
+    mr = 16;
+    if (!gemv_plan(M, ntot, K, nterms, 16, &p)) return hipErrorInvalidValue;
+  }
   w4k::GemvArgs a{};
   a.x = x_planes;
   a.M = (int)M;
@@ -2214,6 +2294,5 @@ hipError_t w4l_gemv_group(const uint16_t* x_planes, int nterms, int n, const int
   a.y = a.gy[0];
   a.N = a.gN[0];
   if (tiles == 0) return hipSuccess;
-  if (m16) return gemv16_launch(a, nst, waves, xpt, (int)tiles, group == 32, st);
-  return gemv_fast_launch(a, nterms, nst, waves, xpt, 1, (int)tiles, group == 32, st);
+  return gemv_fast_launch(a, nterms, mr, p, (int)tiles, group == 32, st);
 }

@@ -34,9 +34,10 @@ bool w4l_gemv_ok(int64_t M, int64_t K, int nterms);
 // 4 < M <= 16 through the same GEMV kernel (bf16 x, small N); w4l_gemv takes it.
 bool w4l_gemv16_ok(int64_t M, int64_t N, int64_t K, int nterms);
 int w4l_gemv_waves(int64_t N, int64_t K);
-bool w4l_gemv_fast_plan(int64_t M, int64_t N, int64_t K, int nterms, int* nst, int* waves, int* xpt, int* tpw);
-// With a pair, only the straight-line plan is used (hipErrorInvalidValue when
-// w4l_gemv_fast_plan fails) and N is ignored.
+// The straight-line decode GEMV (4-row epilogue) takes (M, N, K, nterms).
+bool w4l_gemv_fast_ok(int64_t M, int64_t N, int64_t K, int nterms);
+// With a pair, only the straight-line plans are used (hipErrorInvalidValue when
+// neither holds) and N is ignored.
 hipError_t w4l_gemv(const uint16_t* x_planes, int nterms, const int32_t* pk, const uint16_t* sc,
                     void* y, int y_f32, int64_t M, int64_t N, int64_t K, int32_t group,
                     hipStream_t st, const W4Pair* pair = nullptr);

@@ -191,6 +191,39 @@ def test_linear_one_hot_reproduces_dequant_exactly():
     assert np.all(np.abs(y[:, subnormal] - w[:, subnormal]) <= 8 * 2.0 ** -126)
 
 
+def test_decode_gemv_one_hot_reproduces_dequant_exactly():
+    """The decode GEMV (M <= 4, K % 256 == 0) expands weights with v_fma_mix_f32 from f16
+    nibble pairs, not with the v_dot2 form above.  One-hot rows of x over the first 16
+    columns (all 16 q values, all 8 nibble positions of a word) of 65536 rows, one bf16
+    scale pattern per row: y must equal the bf16 weight exactly for every scale with
+    2^-122 <= |s| < 2^117 (s / 16 normal, 1039 |s| finite) and for s = +-0.  Scales of
+    2^-126..2^-122 (s / 16 subnormal) are outside the stated range; the check there only
+    bounds the error by what flushing s / 16 could cost, 80 * 2^-122."""
+    say("decode GEMV one-hot over all finite scale patterns")
+    N, K = 65536, 256
+    q = np.tile(np.arange(-8, 8, dtype=np.int8), K // 16)[None].repeat(N, 0)
+    s_bits = np.arange(65536, dtype=np.uint32).astype(np.uint16)
+    expo = (s_bits >> 7) & 0xFF
+    exact = ((expo >= 127 - 122) & (expo < 127 + 117)) | ((s_bits & 0x7FFF) == 0)
+    low = (expo >= 1) & (expo < 127 - 122)
+    s_bits = np.where(exact | low, s_bits, 0).astype(np.uint16)   # drop huge, non-finite, subnormal scales
+    sc = np.repeat(s_bits[:, None], K // 32, axis=1).copy()
+    pk = o.pack(q)
+    w = o.bf16_to_f32(o.dequant(pk, sc))                             # [N, K]
+    pkd, scd = dev(pk), dev_u16(sc)
+    for k0 in range(0, 16, 4):
+        x = np.zeros((4, K), dtype=np.uint16)
+        x[np.arange(4), k0 + np.arange(4)] = 0x3F80
+        y = w4a16.linear(dev_u16(x), pkd, scd, out_dtype=torch.float32)
+        torch.cuda.synchronize()
+        y = y.cpu().numpy()                                         # [4, N]
+        ref = w[:, k0:k0 + 4].T
+        bad = np.argwhere(y[:, exact] != ref[:, exact])
+        assert bad.size == 0, (k0, bad[:5].tolist(), [hex(int(v)) for v in s_bits[exact][bad[:5, 1]]])
+        say(f"  columns {k0}..{k0 + 3}: {int(np.sum(y[:, low] != ref[:, low]))} inexact below 2^-122")
+        assert np.all(np.abs(y[:, low] - ref[:, low]) <= 80 * 2.0 ** -122)
+
+
 def test_w3_synth_gate():
     say("W3 synthetic gate (q_proj L0 shape)")
     f = load_fixture("w4_gemm_synth.safetensors")
