@@ -121,11 +121,10 @@ size_t w4a16_workspace_size(int64_t M, int64_t N, int64_t K, int32_t x_dtype) {
   return x_split_bytes(M, K, x_dtype) + splitk_bytes(M, N, K, x_dtype);
 }
 
-int w4a16_linear(const void* x, int32_t x_dtype, const int32_t* pk, const uint16_t* sc, void* y,
-                 int32_t y_dtype, int64_t M, int64_t N, int64_t K, int32_t group, int32_t flags,
-                 void* workspace, size_t ws_bytes, void* stream) {
-  static const char* fn = "w4a16_linear";
-  clear_err();
+namespace {
+// argument checks shared by w4a16_linear and w4a16_linear_noalloc (no HIP call)
+int linear_args(const char* fn, int32_t x_dtype, int32_t y_dtype, int64_t M, int64_t N, int64_t K, int32_t group,
+                int32_t flags) {
   int rc = check_dims(fn, M, N, K);
   if (rc) return rc;
   if ((rc = check_group(fn, K, group))) return rc;
@@ -134,6 +133,17 @@ int w4a16_linear(const void* x, int32_t x_dtype, const int32_t* pk, const uint16
   if (y_dtype != W4A16_DTYPE_BF16 && y_dtype != W4A16_DTYPE_F32)
     return fail(W4A16_EINVAL_ARG, "%s: unknown y_dtype %d", fn, (int)y_dtype);
   if (flags != 0) return fail(W4A16_EINVAL_ARG, "%s: unknown flags 0x%x", fn, (unsigned)flags);
+  return W4A16_OK;
+}
+}  // namespace
+
+int w4a16_linear(const void* x, int32_t x_dtype, const int32_t* pk, const uint16_t* sc, void* y,
+                 int32_t y_dtype, int64_t M, int64_t N, int64_t K, int32_t group, int32_t flags,
+                 void* workspace, size_t ws_bytes, void* stream) {
+  static const char* fn = "w4a16_linear";
+  clear_err();
+  int rc = linear_args(fn, x_dtype, y_dtype, M, N, K, group, flags);
+  if (rc) return rc;
   if (M == 0 || N == 0) return W4A16_OK;
   if ((rc = check_ptr(y, "y", fn))) return rc;
   hipStream_t st = static_cast<hipStream_t>(stream);
@@ -164,6 +174,34 @@ int w4a16_linear(const void* x, int32_t x_dtype, const int32_t* pk, const uint16
                         fn);
   }
   return hip_status(w4l_linear(planes, nterms, pk, sc, y, y_f32, M, N, K, group, st), fn);
+}
+
+int w4a16_linear_noalloc(const void* x, int32_t x_dtype, const int32_t* pk, const uint16_t* sc, void* y,
+                         int32_t y_dtype, int64_t M, int64_t N, int64_t K, int32_t group, int32_t flags,
+                         void* stream) {
+  static const char* fn = "w4a16_linear_noalloc";
+  clear_err();
+  int rc = linear_args(fn, x_dtype, y_dtype, M, N, K, group, flags);
+  if (rc) return rc;
+  if (M == 0 || N == 0) return W4A16_OK;
+  if ((rc = check_ptr(y, "y", fn))) return rc;
+  if (K > 0 && ((rc = check_ptr(x, "x", fn)) || (rc = check_ptr(pk, "pk", fn)) || (rc = check_ptr(sc, "sc", fn))))
+    return rc;
+  const size_t need = x_split_bytes(M, K, x_dtype);
+  if (need > W4L_SCRATCH_BYTES)
+    return fail(W4A16_EWORKSPACE, "%s: f32 activations need %zu bytes of scratch, beyond its %u-byte maximum", fn,
+                need, (unsigned)W4L_SCRATCH_BYTES);
+  void* scratch = nullptr;
+  if ((rc = hip_status(w4l_scratch(&scratch), fn))) return rc;
+  // the same routes as w4a16_linear given a W4L_SCRATCH_BYTES workspace: the f32 planes,
+  // or the split-K partials when they fit (else the one-pass route)
+  rc = w4a16_linear(x, x_dtype, pk, sc, y, y_dtype, M, N, K, group, flags, scratch, W4L_SCRATCH_BYTES, stream);
+  if (rc) {
+    char msg[sizeof g_err];
+    snprintf(msg, sizeof msg, "%s", g_err);
+    return fail(rc, "%s: %s", fn, msg);
+  }
+  return W4A16_OK;
 }
 
 int w4a16_linear_group(const void* x, int32_t x_dtype, int32_t n, const int32_t* const* pk,

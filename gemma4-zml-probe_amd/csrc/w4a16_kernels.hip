@@ -172,9 +172,10 @@ __device__ __forceinline__ bf16x8 dequant8(uint32_t w, uint32_t slo, uint32_t sh
 //   (1024 + n) s - 1032 s = (n - 8) s   or   (1024 + 16 n) (s / 16) - 72 s = (n - 8) s
 // in one rounding of an exact result (both are integer multiples of s with at most
 // 12 significant bits), and v_cvt_pk_bf16_f32 rounds pairs to bf16 (RNE):
-// dequantW4's rounding.  Exact for 2^-122 <= |s| < 2^117 (s / 16 stays normal, and
-// 1039 |s| stays finite) and s = +-0; 17 VALU instructions per 8 weights, 12 of them
-// at half rate, against 19 (12 at half rate) for dequant8.
+// dequantW4's rounding.  Exact for 2^-126 <= |s| < 2^117 (1039 |s| stays finite;
+// below 2^-122, s / 16 is an fp32 denormal, which the kernels keep) and s = +-0;
+// 17 VALU instructions per 8 weights, 12 of them at half rate, against 19 (12 at
+// half rate) for dequant8.
 struct MixScale {
   float s, c1, s16, c2;  // s, -1032 s, s / 16, -72 s
 };

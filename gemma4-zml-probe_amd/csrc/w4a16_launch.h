@@ -74,6 +74,12 @@ hipError_t w4l_gate_up(const uint16_t* x_planes, int nterms, const int32_t* pk_g
 hipError_t w4l_gelu_mul(const float* g, const float* u, void* h, int h_f32, int bf16_dots, int64_t n,
                         hipStream_t st);
 
+// Static device scratch of w4a16_linear_noalloc (w4a16_scratch.hip): W4L_SCRATCH_BYTES
+// bytes per GPU, whose address on the current device this returns (looked up once
+// per device).
+#define W4L_SCRATCH_BYTES (8u << 20)
+hipError_t w4l_scratch(void** ptr);
+
 hipError_t w4l_unpack(const int32_t* pk, int8_t* q, int64_t nwords, hipStream_t st);
 hipError_t w4l_dequant(const int32_t* pk, const uint16_t* sc, uint16_t* w, int64_t N, int64_t K,
                        int32_t group, hipStream_t st);

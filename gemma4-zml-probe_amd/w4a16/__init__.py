@@ -41,7 +41,8 @@ GROUP = 32
 # Every symbol include/w4a16.h declares.
 EXPORTS = ("w4a16_version", "w4a16_last_error", "w4a16_unpack", "w4a16_dequant",
            "w4a16_workspace_size", "w4a16_linear", "w4a16_gate_up_workspace_size",
-           "w4a16_gate_up_gelu", "w4a16_lm_head_workspace_size", "w4a16_lm_head", "w4a16_linear_group")
+           "w4a16_gate_up_gelu", "w4a16_lm_head_workspace_size", "w4a16_lm_head", "w4a16_linear_group",
+           "w4a16_linear_noalloc")
 GATE_UP_BF16_DOTS = 1
 
 
@@ -91,6 +92,8 @@ def lib() -> ctypes.CDLL:
         L.w4a16_lm_head.restype = ctypes.c_int
         L.w4a16_linear_group.argtypes = [P, I32, I32, P, P, P, P, I32, I64, I64, I32, I32, P, ctypes.c_size_t, P]
         L.w4a16_linear_group.restype = ctypes.c_int
+        L.w4a16_linear_noalloc.argtypes = [P, I32, P, P, P, I32, I64, I64, I64, I32, I32, P]
+        L.w4a16_linear_noalloc.restype = ctypes.c_int
         _lib = L
     return _lib
 

@@ -117,13 +117,13 @@ size_t w4a16_workspace_size(int64_t M, int64_t N, int64_t K, int32_t x_dtype);
  * (RNE_bf16(q * s)); products with x are exact and accumulate in fp32, as in
  * dotPrec with fam = null (engine.zig:531-532).  Only the summation order
  * differs from the reference.
- * Scale range: the in-register dequant is exact for 2^-126 <= |s| < 2^120 and
+ * Scale range: the in-register dequant is exact for 2^-126 <= |s| < 2^117 and
  * s = +-0, which holds for every scale a quantizer writes (max|w| / 7.5 of a
  * finite bf16 row group).  Outside it the fused kernels may differ from
- * w4a16_dequant followed by a dot: a subnormal scale is flushed to zero (its
- * group's weights count as 0), and from |s| >= 2^120 the expansion's fp32
- * intermediate (128 + n) * s may overflow, so such scales (and +-inf / NaN
- * ones) can give +-inf or NaN outputs.  w4a16_dequant is exact for every bit
+ * w4a16_dequant followed by a dot: a subnormal scale may be flushed to zero (its
+ * group's weights count as 0), and from |s| >= 2^117 the expansion's fp32
+ * intermediates ((1024 + n) * s in the decode GEMV, (128 + n) * s elsewhere) may
+ * overflow, so such scales (and +-inf / NaN ones) can give +-inf or NaN outputs.  w4a16_dequant is exact for every bit
  * pattern.  The same holds for w4a16_linear_group and w4a16_gate_up_gelu.
  *   x_dtype  W4A16_DTYPE_BF16 or W4A16_DTYPE_F32 (the
  *            engine's f32 activations; carried exactly as a sum of three bf16
@@ -142,6 +142,27 @@ int w4a16_linear(const void *x, int32_t x_dtype,
                  void *y, int32_t y_dtype,
                  int64_t M, int64_t N, int64_t K, int32_t group,
                  int32_t flags, void *workspace, size_t ws_bytes, void *stream);
+
+/*
+ * w4a16_linear without a workspace argument, for callers that cannot allocate
+ * device memory (code under HIP graph capture, tight serving loops, harnesses that
+ * forbid hipMalloc).  No counterpart in the reference (its dequant temporaries
+ * live in the XLA arena).  It allocates nothing and calls no allocating routine:
+ * the f32-activation planes and the split-K partial sums that w4a16_linear keeps in
+ * the caller's workspace go to a static device array of 8 MiB per GPU, held until
+ * the process ends (its address is looked up once per device, on the first call
+ * with that device current).  Same results as w4a16_linear given an 8 MiB
+ * workspace: f32 x needs 6 * M * K <= 8 MiB (rounded up to 256), else
+ * W4A16_EWORKSPACE before any HIP call; bf16 x takes the split-K route when its
+ * partials fit, else the one-pass route.  Every call on one GPU shares that array:
+ * calls that overlap on one GPU (different streams without ordering between them)
+ * race.  The stream must belong to the current device.
+ */
+int w4a16_linear_noalloc(const void *x, int32_t x_dtype,
+                         const int32_t *pk, const uint16_t *sc,
+                         void *y, int32_t y_dtype,
+                         int64_t M, int64_t N, int64_t K, int32_t group,
+                         int32_t flags, void *stream);
 
 /*
  * Several linears that read the same activations, y_j[M, N_j] = x[M, K] .
