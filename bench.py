@@ -51,6 +51,36 @@ def log(*a):
     print(*a, file=sys.stderr, flush=True)
 
 
+def build_info() -> dict:
+    """What __graft_entry__.build() recorded next to libw4a16.so (git commit of the
+    sources, dirty flag, build time, compiler flags), or {}."""
+    try:
+        with open(os.path.join(ROOT, "gemma4-zml-probe_amd", "build_info.json")) as f:
+            return json.load(f)
+    except (OSError, ValueError):
+        return {}
+
+
+def gpu_clocks() -> str:
+    """Current / highest shader (sclk) and memory (mclk) clock levels of the first GPU,
+    from its sysfs DPM tables ('*' marks the current level), or '?'."""
+    import glob
+    for dev in sorted(glob.glob("/sys/class/drm/card*/device")):
+        out = []
+        for name in ("pp_dpm_sclk", "pp_dpm_mclk"):
+            try:
+                with open(os.path.join(dev, name)) as f:
+                    lines = [ln.strip() for ln in f if ln.strip()]
+            except OSError:
+                break
+            cur = [ln.split(":", 1)[1].replace("*", "").strip() for ln in lines if ln.endswith("*")]
+            top = lines[-1].split(":", 1)[1].replace("*", "").strip() if lines else "?"
+            out.append(f"{name[-4:]}={cur[0] if cur else '?'}(max {top})")
+        if len(out) == 2:
+            return ",".join(out)
+    return "?"
+
+
 def read_traffic():
     """HBM bytes per launch of the dominant kernel, from the committed rocprofv3
     --pmc summary (line 'traffic_bytes_per_launch: <int>'), or None."""
@@ -74,10 +104,11 @@ def make_set(torch, o, K, N, seed):
     return pkd, scd
 
 
-def synth_x_dev(torch, o, M, K):
-    import numpy as np
-    x = o.synth_x(M, K)
-    return torch.from_numpy(x.view(np.int16)).view(torch.bfloat16).cuda()
+def synth_x_dev(torch, o, M, K, seed=None):
+    """Activations bf16(N(0,1)) [M, K] drawn on the GPU (seed 2000 + M by default)."""
+    g = torch.Generator(device="cuda")
+    g.manual_seed(2000 + M if seed is None else seed)
+    return torch.randn((M, K), generator=g, device="cuda").to(torch.bfloat16)
 
 
 def graph_of(torch, fn):
@@ -143,52 +174,111 @@ def time_config(torch, w4a16, o, M, K, N, launches=None):
             "sets": nsets, "launches": launches}
 
 
-def cpu_baseline(budget_s: float = 15.0):
-    """The reference's CPU path (PyTorch restatement, oracle/cpu_path.py) on the
-    host cores: dequant + matmul per call, over the same 12B layer linears at
-    M=1 (one decode layer per step), repeated until ~budget_s seconds."""
-    import numpy as np
-    import torch
-    from oracle import cpu_path, w4a16_oracle as o
+def cpu_threads() -> int:
+    """Threads for the CPU legs: the CPUs this process may run on (its affinity set),
+    capped by OMP_NUM_THREADS when set -- the GPU box gives a job a share of the
+    host's cores (16 per GPU) while os.cpu_count() reports the whole host."""
+    try:
+        n = len(os.sched_getaffinity(0))
+    except (AttributeError, OSError):
+        n = os.cpu_count() or 1
+    omp = os.environ.get("OMP_NUM_THREADS", "")
+    if omp.isdigit() and int(omp) > 0:
+        n = min(n, int(omp))
+    return max(1, n)
 
-    torch.set_num_threads(max(1, torch.get_num_threads()))
-    mats = []
-    g = torch.Generator()
-    g.manual_seed(8000)
-    for i, (name, K, N) in enumerate(LAYER_12B):
-        pk = torch.randint(-2**31, 2**31, (N, K // 8), generator=g, dtype=torch.int64).to(torch.int32)
-        sc = (torch.randn((N, K // 32), generator=g).abs() * 0.02).to(torch.bfloat16)
-        mats.append((pk, sc, torch.from_numpy(o.synth_x(1, K).view(np.int16)).view(torch.bfloat16)))
-    step_bytes = sum(lin_bytes(1, K, N) for _, K, N in LAYER_12B)
 
-    def one_step():
-        for pk, sc, x in mats:
-            cpu_path.linear(x, pk, sc).to(torch.bfloat16)
-
-    one_step()  # warm-up
-    times = []
-    t_start = time.perf_counter()
-    while True:
-        t0 = time.perf_counter()
-        one_step()
-        times.append(time.perf_counter() - t0)
-        if time.perf_counter() - t_start > budget_s or len(times) >= 50:
-            break
-    med = statistics.median(times)
-    cpu_model = ""
+def cpu_model() -> str:
     try:
         with open("/proc/cpuinfo") as f:
             for line in f:
                 if line.startswith("model name"):
-                    cpu_model = line.split(":", 1)[1].strip()
-                    break
+                    return line.split(":", 1)[1].strip()
     except OSError:
         pass
-    return {"value": round(step_bytes / med / 1e9, 4), "unit": "GB/s", "cores": torch.get_num_threads(),
-            "kind": "port",
+    return platform.processor() or "?"
+
+
+# BASELINE.json configs for the CPU legs: name -> list of (M, K, N) linears per run
+CPU_CONFIGS = {
+    "C1": [(1, 1536, 6144)],
+    "C2": [(1, K, N) for K, N in [(1536, 2048), (1536, 256), (1536, 256), (2048, 1536), (1536, 12288), (6144, 1536)]],
+    "C3": [(1, K, N) for _, K, N in LAYER_12B],
+    **{f"C4_M{M}": [(M, K, N) for _, K, N in LAYER_12B] for M in (8, 16, 32, 64)},
+    "C5": [(2048, 3840, 30720), (2048, 15360, 3840)],
+}
+
+
+def cpu_config(name: str, budget_s: float, min_runs: int = 10, warmup: int = 3):
+    """Both CPU legs of one config on the host cores: the
+    reference's dequant + matmul per call (oracle/cpu_path.py), and the matmul alone on
+    weights dequantized beforehand; median, p10 and p90 over >= min_runs runs (fewer
+    when one run exceeds budget_s / min_runs, never fewer than 3) after `warmup` runs."""
+    import torch
+    from oracle import cpu_path
+
+    torch.set_num_threads(cpu_threads())
+    g = torch.Generator()
+    g.manual_seed(8000)
+    mats = []
+    for M, K, N in CPU_CONFIGS[name]:
+        pk = torch.randint(-2**31, 2**31, (N, K // 8), generator=g, dtype=torch.int64).to(torch.int32)
+        sc = (torch.randn((N, K // 32), generator=g).abs() * 0.02).to(torch.bfloat16)
+        x = torch.randn((M, K), generator=g).to(torch.bfloat16)
+        mats.append((pk, sc, x))
+    nbytes = sum(lin_bytes(M, K, N) for M, K, N in CPU_CONFIGS[name])
+    flops = sum(2 * M * N * K for M, K, N in CPU_CONFIGS[name])
+
+    def dq_mm():
+        for pk, sc, x in mats:
+            cpu_path.linear(x, pk, sc).to(torch.bfloat16)
+
+    wf = None
+
+    def mm():
+        for (pk, sc, x), w in zip(mats, wf):
+            (x.to(torch.float32) @ w.t()).to(torch.bfloat16)
+
+    def measure(fn):
+        for _ in range(warmup):
+            fn()
+        times = []
+        t_start = time.perf_counter()
+        while len(times) < min_runs:
+            t0 = time.perf_counter()
+            fn()
+            times.append(time.perf_counter() - t0)
+            if len(times) >= 3 and time.perf_counter() - t_start > budget_s:
+                break
+        times.sort()
+        q = lambda f: times[min(len(times) - 1, int(f * len(times)))]  # noqa: E731
+        return {"median_ms": round(statistics.median(times) * 1e3, 3), "p10_ms": round(q(0.1) * 1e3, 3),
+                "p90_ms": round(q(0.9) * 1e3, 3), "runs": len(times)}
+
+    legs = {"dequant_matmul": measure(dq_mm)}
+    wf = [cpu_path.dequant(pk, sc).to(torch.float32) for pk, sc, _ in mats]
+    legs["matmul_only"] = measure(mm)
+    for leg in legs.values():
+        t = leg["median_ms"] * 1e-3
+        leg["GBps"] = round(nbytes / t / 1e9, 4)
+        leg["GFLOPs"] = round(flops / t / 1e9, 2)
+    return {"config": name, "bytes": nbytes, "flops": flops, "threads": torch.get_num_threads(), **legs}
+
+
+def cpu_baseline(budget_s: float = 15.0):
+    """The reference's CPU path (PyTorch restatement, oracle/cpu_path.py) on the host
+    cores for the headline workload (configs[2], one 12B decode layer's linears at
+    M=1): dequant + matmul per call, plus the matmul-only leg."""
+    r = cpu_config("C3", budget_s)
+    d, m = r["dequant_matmul"], r["matmul_only"]
+    return {"value": d["GBps"], "unit": "GB/s", "cores": r["threads"], "kind": "port",
+            "matmul_only": m["GBps"],
             "sample": f"one 12B decode layer's 6 W4A16 linears at M=1 (q,k,v,o,gate_up,down), torch CPU "
-                      f"dequant+matmul per call (oracle/cpu_path.py), median of {len(times)} steps, "
-                      f"{med * 1e3:.1f} ms/step; os.cpu_count()={os.cpu_count()}; cpu={cpu_model}"}
+                      f"dequant+matmul per call (oracle/cpu_path.py): median {d['median_ms']} ms/step "
+                      f"(p10 {d['p10_ms']}, p90 {d['p90_ms']}, {d['runs']} runs after 3 warm-ups); matmul only on "
+                      f"pre-dequantized weights: median {m['median_ms']} ms/step ({m['GBps']} GB/s); "
+                      f"threads {r['threads']} (affinity {len(os.sched_getaffinity(0))}, "
+                      f"os.cpu_count() {os.cpu_count()}); cpu={cpu_model()}"}
 
 
 def time_gate_up(torch, w4a16, o, M, K, F, unfused_leg=True):
@@ -268,6 +358,8 @@ def main() -> int:
     ap.add_argument("--all", action="store_true", help="also sweep every BASELINE config (stderr + gpurun_out)")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--cpu-budget", type=float, default=15.0)
+    ap.add_argument("--cpu-configs", action="store_true",
+                    help="also time both CPU legs (dequant+matmul, matmul only) of every BASELINE config C1-C5")
     ap.add_argument("--only-dominant", action="store_true",
                     help="run only the dominant kernel's timing (gate_up, M=1): the workload of the committed "
                          "rocprofv3 kernel-trace and --pmc summaries")
@@ -295,12 +387,15 @@ def main() -> int:
 
     import torch
     import w4a16
-    from oracle import w4a16_oracle as o
 
+    o = None  # the timed paths build their inputs with torch; only the CPU legs use oracle/
     w4a16.lib()  # fails loudly without the HIP library
     props = torch.cuda.get_device_properties(0)
-    log(f"BUILD: device={props.name} arch={getattr(props, 'gcnArchName', '?')} CUs={props.multi_processor_count} "
-        f"hip={torch.version.hip} torch={torch.__version__} lib=libw4a16.so(-O3, gfx950) host={platform.node()}")
+    bi = build_info()
+    log(f"BUILD: git={bi.get('git', '?')}{'-dirty' if bi.get('dirty') else ''} built={bi.get('built', '?')} "
+        f"flags=\"{bi.get('flags', '?')}\" device={props.name} arch={getattr(props, 'gcnArchName', '?')} "
+        f"CUs={props.multi_processor_count} clocks={gpu_clocks()} hip={torch.version.hip} torch={torch.__version__} "
+        f"host={platform.node()}")
 
     if args.copy_calibration:
         n = 64 * 2**20
@@ -383,24 +478,31 @@ def main() -> int:
     g = graph_of(torch, lambda: [step(s) for s in range(nsets)])
     reps = max(1, -(-args.steps // nsets))
     steady(torch, g)
-    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    # an event after every replay: the replay times give the step-time distribution
+    ev = [torch.cuda.Event(enable_timing=True) for _ in range(reps + 1)]
+    torch.cuda.synchronize()
     t0 = time.perf_counter()
-    e0.record()
-    for _ in range(reps):
+    ev[0].record()
+    for r in range(reps):
         g.replay()
-    e1.record()
+        ev[r + 1].record()
     torch.cuda.synchronize()
     dt_wall = time.perf_counter() - t0
     n_steps = reps * nsets
-    dt = e0.elapsed_time(e1) * 1e-3
+    dt = ev[0].elapsed_time(ev[-1]) * 1e-3
     ms_per_step = dt / n_steps * 1e3
     value = step_bytes / (dt / n_steps) / 1e9
+    per_step_us = sorted(ev[r].elapsed_time(ev[r + 1]) * 1e3 / nsets for r in range(reps))
+    q = lambda f: per_step_us[min(len(per_step_us) - 1, int(f * len(per_step_us)))]  # noqa: E731
+    dist = {"mean": round(dt / n_steps * 1e6, 3), "median": round(statistics.median(per_step_us), 3),
+            "p10": round(q(0.1), 3), "p90": round(q(0.9), 3), "replays": reps, "steps_per_replay": nsets}
     del g
 
     # dominant kernel: graph of back-to-back gate_up launches over >= 8 weight sets
     dom_name, dK, dN = LAYER_12B[dom]
     dom = time_config(torch, w4a16, o, 1, dK, dN)
     dom_bytes, dom_avg, dom_gbs = dom["bytes"], dom["us"] * 1e-6, dom["GBps"]
+    log(f"step us: median {dist['median']} p10 {dist['p10']} p90 {dist['p90']} over {reps} replays of {nsets} steps")
     log(f"step: {ms_per_step * 1e3:.2f} us ({value:.1f} GB/s, {value / PEAK_HBM_GBS * 100:.1f} % of HBM peak), "
         f"wall {dt_wall / n_steps * 1e6:.2f} us/step, eager {eager_ms * 1e3:.1f} us/step; "
         f"gate_up launch avg {dom_avg * 1e6:.2f} us = {dom_gbs:.1f} GB/s")
@@ -423,6 +525,8 @@ def main() -> int:
         cfgs += [("12B_full_q", 1, 3840, 8192), ("12B_full_k", 1, 3840, 512), ("12B_full_o", 1, 8192, 3840)]
         # E2B per-layer-embedding linears (engine.zig:659, 661, 723)
         cfgs += [("E2B_ple_gate", 1, 1536, 256), ("E2B_ple_proj", 1, 256, 1536), ("E2B_plmp", 1, 1536, 8960)]
+        # E2B double-wide MLP of the KV-shared layers 15-34: gate + up 1536->12288 each, down 12288->1536
+        cfgs += [("E2B_dw_gate_up", 1, 1536, 24576), ("E2B_dw_down", 1, 12288, 1536)]
         cfgs += [(f"C4_M{M}", M, 3840, 30720) for M in (8, 16, 32, 64)]
         # configs[3] covers every config-2 weight at M = 8..64: the other linears of the layer
         cfgs += [(f"C4_{n}_M{M}", M, K, N) for M in (8, 16, 32, 64)
@@ -435,7 +539,7 @@ def main() -> int:
             log(f"{name:12s} M={M:5d} K={K:6d} N={N:6d}  {r['us']:9.2f} us"
                 f"  {r['GBps']:8.1f} GB/s ({r['hbm_frac'] * 100:5.1f} %)  {r['TFLOPs']:8.2f} TFLOP/s ({r['mfma_frac'] * 100:5.1f} %)")
         # fused gate/up + gelu*mul (engine.zig:653) against the unfused composition
-        for name, M, K, F in [("E2B_gelu", 1, 1536, 6144), ("12B_gelu", 1, 3840, 15360),
+        for name, M, K, F in [("E2B_gelu", 1, 1536, 6144), ("E2B_dw_gelu", 1, 1536, 12288), ("12B_gelu", 1, 3840, 15360),
                               ("12B_gelu", 64, 3840, 15360), ("12B_gelu", 2048, 3840, 15360)]:
             r = time_gate_up(torch, w4a16, o, M, K, F)
             r["name"] = name
@@ -449,6 +553,19 @@ def main() -> int:
     cpu = None if args.no_cpu else cpu_baseline(args.cpu_budget)
     if cpu:
         log(f"cpu baseline: {cpu['value']} GB/s on {cpu['cores']} threads ({cpu['sample']})")
+    cpu_table = None
+    if (args.all or args.cpu_configs) and not args.no_cpu:
+        cpu_table = []
+        for name in CPU_CONFIGS:
+            r = cpu_config(name, args.cpu_budget)
+            cpu_table.append(r)
+            d, m = r["dequant_matmul"], r["matmul_only"]
+            log(f"cpu {name:7s} dequant+matmul {d['median_ms']:10.3f} ms ({d['GBps']:8.3f} GB/s, {d['GFLOPs']:8.2f} GFLOP/s)"
+                f"  matmul only {m['median_ms']:10.3f} ms ({m['GBps']:8.3f} GB/s, {m['GFLOPs']:8.2f} GFLOP/s)"
+                f"  threads {r['threads']}")
+        os.makedirs(os.path.join(ROOT, "gpurun_out"), exist_ok=True)
+        with open(os.path.join(ROOT, "gpurun_out", "cpu_configs.json"), "w") as f:
+            json.dump(cpu_table, f, indent=1)
 
     traffic = read_traffic()
     out = {
@@ -467,8 +584,12 @@ def main() -> int:
         "cpu_baseline": cpu,
         "m64": {"TFLOPs": round(m64["TFLOPs"], 2), "mfma_frac": round(m64["mfma_frac"], 4),
                 "GBps": round(m64["GBps"], 1), "us": round(m64["us"], 2)},
-        "timing": {"method": "HIP graph replays, events around the timed region", "eager_us_per_step": round(eager_ms * 1e3, 2)},
+        "timing": {"method": "HIP graph replays, events around the timed region and after every replay",
+                   "step_us": dist, "eager_us_per_step": round(eager_ms * 1e3, 2)},
+        "build": {"git": bi.get("git"), "dirty": bi.get("dirty"), "clocks": gpu_clocks()},
     }
+    if cpu_table is not None:
+        out["cpu_configs"] = cpu_table
     if table is not None:
         out["sweep"] = [{k: (round(v, 3) if isinstance(v, float) else v) for k, v in r.items()} for r in table]
     print(json.dumps(out), flush=True)

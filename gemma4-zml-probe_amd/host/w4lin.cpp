@@ -132,14 +132,14 @@ void W4Lin::linear_f32(const float* x, float* y, int64_t m, void* workspace, siz
 }
 
 namespace {
-void gate_up_call(const W4Lin& gate, const W4Lin& up, const uint16_t* x, void* h, int32_t h_dtype, int64_t m,
-                  void* workspace, size_t ws_bytes, hipStream_t stream, bool bf16_dots) {
+void gate_up_call(const W4Lin& gate, const W4Lin& up, const void* x, int32_t x_dtype, void* h, int32_t h_dtype,
+                  int64_t m, void* workspace, size_t ws_bytes, hipStream_t stream, bool bf16_dots) {
   if (up.n != gate.n || up.k != gate.k || up.group != gate.group)
     throw Error(W4A16_EINVAL_SHAPE, "gate_up_gelu: up [" + std::to_string(up.n) + ", " + std::to_string(up.k) +
                                         "] / group " + std::to_string(up.group) + " does not match gate [" +
                                         std::to_string(gate.n) + ", " + std::to_string(gate.k) + "] / group " +
                                         std::to_string(gate.group));
-  check(w4a16_gate_up_gelu(x, W4A16_DTYPE_BF16, gate.pk, gate.sc, up.pk, up.sc, h, h_dtype, m, gate.n, gate.k,
+  check(w4a16_gate_up_gelu(x, x_dtype, gate.pk, gate.sc, up.pk, up.sc, h, h_dtype, m, gate.n, gate.k,
                            gate.group, bf16_dots ? W4A16_GATE_UP_BF16_DOTS : 0, workspace, ws_bytes, stream),
         "gate_up_gelu");
 }
@@ -151,12 +151,21 @@ size_t gate_up_workspace(const W4Lin& gate, int64_t m) {
 
 void gate_up_gelu(const W4Lin& gate, const W4Lin& up, const uint16_t* x, uint16_t* h, int64_t m, void* workspace,
                   size_t ws_bytes, hipStream_t stream, bool bf16_dots) {
-  gate_up_call(gate, up, x, h, W4A16_DTYPE_BF16, m, workspace, ws_bytes, stream, bf16_dots);
+  gate_up_call(gate, up, x, W4A16_DTYPE_BF16, h, W4A16_DTYPE_BF16, m, workspace, ws_bytes, stream, bf16_dots);
 }
 
 void gate_up_gelu(const W4Lin& gate, const W4Lin& up, const uint16_t* x, float* h, int64_t m, void* workspace,
                   size_t ws_bytes, hipStream_t stream, bool bf16_dots) {
-  gate_up_call(gate, up, x, h, W4A16_DTYPE_F32, m, workspace, ws_bytes, stream, bf16_dots);
+  gate_up_call(gate, up, x, W4A16_DTYPE_BF16, h, W4A16_DTYPE_F32, m, workspace, ws_bytes, stream, bf16_dots);
+}
+
+size_t gate_up_workspace_f32(const W4Lin& gate, int64_t m) {
+  return w4a16_gate_up_workspace_size(m, gate.n, gate.k, W4A16_DTYPE_F32);
+}
+
+void gate_up_gelu_f32(const W4Lin& gate, const W4Lin& up, const float* x, float* h, int64_t m, void* workspace,
+                      size_t ws_bytes, hipStream_t stream) {
+  gate_up_call(gate, up, x, W4A16_DTYPE_F32, h, W4A16_DTYPE_F32, m, workspace, ws_bytes, stream, false);
 }
 
 void linear_group(const std::vector<W4Lin>& lins, const uint16_t* x, const std::vector<uint16_t*>& ys, int64_t m,
@@ -170,9 +179,10 @@ size_t linear_group_workspace(const std::vector<W4Lin>& lins, int64_t m) {
   return ws;
 }
 
-void linear_group(const std::vector<W4Lin>& lins, const uint16_t* x, const std::vector<uint16_t*>& ys, int64_t m,
-                  void* workspace, size_t ws_bytes, hipStream_t stream) {
-  if (lins.empty() || lins.size() > 4 || ys.size() != lins.size())
+namespace {
+void group_call(const std::vector<W4Lin>& lins, const void* x, int32_t x_dtype, void* const* ys, size_t nys,
+                int32_t y_dtype, int64_t m, void* workspace, size_t ws_bytes, hipStream_t stream) {
+  if (lins.empty() || lins.size() > 4 || nys != lins.size())
     throw Error(W4A16_EINVAL_ARG, "linear_group: 1 to 4 linears, one output each");
   const int32_t* pk[4];
   const uint16_t* sc[4];
@@ -186,9 +196,26 @@ void linear_group(const std::vector<W4Lin>& lins, const uint16_t* x, const std::
     y[j] = ys[j];
     n[j] = lins[j].n;
   }
-  check(w4a16_linear_group(x, W4A16_DTYPE_BF16, (int32_t)lins.size(), pk, sc, y, n, W4A16_DTYPE_BF16, m,
-                           lins[0].k, lins[0].group, 0, workspace, ws_bytes, stream),
+  check(w4a16_linear_group(x, x_dtype, (int32_t)lins.size(), pk, sc, y, n, y_dtype, m, lins[0].k, lins[0].group, 0,
+                           workspace, ws_bytes, stream),
         "linear_group");
+}
+}  // namespace
+
+void linear_group(const std::vector<W4Lin>& lins, const uint16_t* x, const std::vector<uint16_t*>& ys, int64_t m,
+                  void* workspace, size_t ws_bytes, hipStream_t stream) {
+  std::vector<void*> y(ys.begin(), ys.end());
+  group_call(lins, x, W4A16_DTYPE_BF16, y.data(), y.size(), W4A16_DTYPE_BF16, m, workspace, ws_bytes, stream);
+}
+
+size_t linear_group_workspace_f32(const std::vector<W4Lin>& lins, int64_t m) {
+  return lins.empty() ? 0 : w4a16_workspace_size(m, 0, lins[0].k, W4A16_DTYPE_F32);
+}
+
+void linear_group_f32(const std::vector<W4Lin>& lins, const float* x, const std::vector<float*>& ys, int64_t m,
+                      void* workspace, size_t ws_bytes, hipStream_t stream) {
+  std::vector<void*> y(ys.begin(), ys.end());
+  group_call(lins, x, W4A16_DTYPE_F32, y.data(), y.size(), W4A16_DTYPE_F32, m, workspace, ws_bytes, stream);
 }
 
 size_t lm_head_workspace(int64_t m, int64_t v, int64_t k, int topk) {

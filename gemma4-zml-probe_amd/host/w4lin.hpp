@@ -98,6 +98,13 @@ void gate_up_gelu(const W4Lin& gate, const W4Lin& up, const uint16_t* x, uint16_
 void gate_up_gelu(const W4Lin& gate, const W4Lin& up, const uint16_t* x, float* h, int64_t m, void* workspace,
                   size_t ws_bytes, hipStream_t stream, bool bf16_dots = false);
 
+// The same with f32 activations (dotPrec with fam = null: xff stays in the compute
+// dtype, engine.zig:530-533): x f32 [m, K], h f32; gate_up_workspace_f32(gate, m) bytes
+// of workspace are required (the three bf16 planes of x).
+size_t gate_up_workspace_f32(const W4Lin& gate, int64_t m);
+void gate_up_gelu_f32(const W4Lin& gate, const W4Lin& up, const float* x, float* h, int64_t m, void* workspace,
+                      size_t ws_bytes, hipStream_t stream);
+
 // Linears that read the same x (q, k, v at engine.zig:552,571,583): ys[j][m, lins[j].n] =
 // x . lins[j].toW()^T, one launch at decode; 1..4 linears with the same k and group.
 void linear_group(const std::vector<W4Lin>& lins, const uint16_t* x, const std::vector<uint16_t*>& ys, int64_t m,
@@ -108,6 +115,11 @@ void linear_group(const std::vector<W4Lin>& lins, const uint16_t* x, const std::
 size_t linear_group_workspace(const std::vector<W4Lin>& lins, int64_t m);
 void linear_group(const std::vector<W4Lin>& lins, const uint16_t* x, const std::vector<uint16_t*>& ys, int64_t m,
                   void* workspace, size_t ws_bytes, hipStream_t stream);
+// f32 activations, f32 outputs (the fam = null flow): linear_group_workspace_f32(lins, m)
+// bytes of workspace are required.
+size_t linear_group_workspace_f32(const std::vector<W4Lin>& lins, int64_t m);
+void linear_group_f32(const std::vector<W4Lin>& lins, const float* x, const std::vector<float*>& ys, int64_t m,
+                      void* workspace, size_t ws_bytes, hipStream_t stream);
 
 // The decode head (engine.zig:765-766) and its topK (gemma4_g12auto.zig:1532): logits[m, v] =
 // softcap * tanh(x . embed^T / softcap) (f32), top-k values (descending, ties by index) and

@@ -15,16 +15,30 @@
 //   w4lin_tool qkv <file.safetensors> <prefix> <j> <M> <x.bin> <out_prefix>
 //       q, k (and v on sliding layers) of layer j as one grouped call (engine.zig:552-583);
 //       writes <out_prefix>.q.bin, .k.bin[, .v.bin] (bf16).
+//   w4lin_tool chain <file.safetensors> <prefix> <j> <M> <g12|e2b> <bf16|f32> <in_prefix> <out_prefix>
+//       the linears of decoder layer j in engine order (engine.zig:552-663): q, k, v as one
+//       grouped call on x (per the model's wiring: 12B full layers have no v, g12.zig;
+//       E2B KV-shared layers j >= 15 only q, engine.zig:560-567), o on the attention
+//       context a, gate_up_gelu on xff, down fed by its output h, and for E2B the
+//       per-layer-embedding pair: pg = h2 . per_layer_input_gate^T, g = gelu(pg) * ple
+//       (host f32, the engine's elementwise glue), then g . per_layer_projection^T.
+//       Flow bf16 is dotPrec with fam = bf16 (bf16 inputs and outputs, h and g rounded to
+//       bf16 before their consumer); flow f32 is fam = null (f32 throughout).
+//       Reads <in>.x/.a/.xff[/.h2].bin (bf16 or f32 per flow) and <in>.ple.bin (f32);
+//       writes <out>.q/.k/.v/.o/.h/.mlp[/.pg/.g/.ple].bin in the flow's dtype.
 //   w4lin_tool head <file.safetensors> <embed_name> <M> <x.bin> <softcap> <topk> <out_prefix>
 //       logits (f32) and top-k of the tied-embedding head (engine.zig:765-766);
 //       writes <out_prefix>.logits.bin, .values.bin (f32), .indices.bin (i32).
 #include <hip/hip_runtime.h>
 
+#include <algorithm>
+#include <cmath>
 #include <cstdio>
 #include <cstdlib>
 #include <cstring>
 #include <fstream>
 #include <iostream>
+#include <memory>
 #include <string>
 #include <vector>
 
@@ -40,7 +54,8 @@ int usage() {
                "       w4lin_tool dequant <file> <name> <w.bin>\n"
                "       w4lin_tool mlp <file> <gate> <up> <M> <x.bin> <h.bin> [bf16|f32]\n"
                "       w4lin_tool qkv <file> <prefix> <j> <M> <x.bin> <out_prefix>\n"
-               "       w4lin_tool head <file> <embed_name> <M> <x.bin> <softcap> <topk> <out_prefix>\n");
+               "       w4lin_tool head <file> <embed_name> <M> <x.bin> <softcap> <topk> <out_prefix>\n"
+               "       w4lin_tool chain <file> <prefix> <j> <M> <g12|e2b> <bf16|f32> <in_prefix> <out_prefix>\n");
   return 2;
 }
 
@@ -246,6 +261,171 @@ int cmd_head(int argc, char** argv) {
   return 0;
 }
 
+// Device buffer freed on scope exit.
+struct DevBuf {
+  void* p = nullptr;
+  size_t n = 0;
+  explicit DevBuf(size_t bytes) : n(bytes) { hip_ok(hipMalloc(&p, std::max<size_t>(bytes, 16)), "hipMalloc"); }
+  ~DevBuf() { (void)hipFree(p); }
+  DevBuf(const DevBuf&) = delete;
+  DevBuf& operator=(const DevBuf&) = delete;
+  template <class T>
+  T* as() const { return static_cast<T*>(p); }
+  void upload(const std::vector<char>& h) { hip_ok(hipMemcpy(p, h.data(), h.size(), hipMemcpyHostToDevice), "upload"); }
+  std::vector<char> download() const {
+    std::vector<char> h(n);
+    hip_ok(hipMemcpy(h.data(), p, n, hipMemcpyDeviceToHost), "download");
+    return h;
+  }
+};
+
+float bf16_bits_to_float(uint16_t h) {
+  const uint32_t u = (uint32_t)h << 16;
+  float f;
+  std::memcpy(&f, &u, 4);
+  return f;
+}
+
+uint16_t float_to_bf16_rne(float f) {
+  uint32_t u;
+  std::memcpy(&u, &f, 4);
+  if ((u & 0x7fffffffu) > 0x7f800000u) return 0x7fc0;
+  return (uint16_t)((u + 0x7fffu + ((u >> 16) & 1u)) >> 16);
+}
+
+// gelu with the tanh approximation (ZML's Tensor.gelu), in double, rounded to f32.
+float gelu_tanh_host(float g) {
+  const double x = g, z = 0.7978845608028654 * (x + 0.044715 * x * x * x);
+  return (float)(x / (1.0 + std::exp(-2.0 * z)));
+}
+
+int cmd_chain(int argc, char** argv) {
+  if (argc < 10) return usage();
+  const std::string prefix = argv[3], model = argv[6], flow = argv[7], in = argv[8], out = argv[9];
+  const int j = std::atoi(argv[4]);
+  const int64_t M = std::atoll(argv[5]);
+  if ((model != "g12" && model != "e2b") || (flow != "bf16" && flow != "f32") || M < 1) return usage();
+  const bool e2b = model == "e2b", f32 = flow == "f32";
+  const size_t es = f32 ? 4 : 2;
+  w4::DeviceStore store(argv[2]);
+  const std::string l = prefix + "." + std::to_string(j) + ".";
+  // q/k/v wiring: 12B full layers take V from k_proj (no v_proj, g12.zig); E2B layers from
+  // first_kv_shared = 15 on read the writer's cache and project only q (engine.zig:560-567).
+  std::vector<std::string> qkv = {"q"};
+  if (!(e2b && j >= 15)) {
+    qkv.push_back("k");
+    if (e2b || !w4::g12_is_full(j)) qkv.push_back("v");
+  }
+  std::vector<w4::W4Lin> lins;
+  for (const auto& n : qkv) lins.push_back(w4::W4Lin::init(store, l + "self_attn." + n + "_proj"));
+  const w4::W4Lin o = w4::W4Lin::init(store, l + "self_attn.o_proj");
+  const w4::W4Lin gate = w4::W4Lin::init(store, l + "mlp.gate_proj");
+  const w4::W4Lin up = w4::W4Lin::init(store, l + "mlp.up_proj");
+  const w4::W4Lin down = w4::W4Lin::init(store, l + "mlp.down_proj");
+  const int64_t D = lins[0].k;
+
+  DevBuf x(M * D * es), a(M * o.k * es), xff(M * gate.k * es);
+  x.upload(read_file(in + ".x.bin", x.n));
+  a.upload(read_file(in + ".a.bin", a.n));
+  xff.upload(read_file(in + ".xff.bin", xff.n));
+
+  // q, k, v: one grouped call
+  std::vector<std::unique_ptr<DevBuf>> ys;
+  for (const auto& lin : lins) ys.emplace_back(new DevBuf(M * lin.n * es));
+  if (f32) {
+    DevBuf ws(w4::linear_group_workspace_f32(lins, M));
+    std::vector<float*> yp;
+    for (auto& y : ys) yp.push_back(y->as<float>());
+    w4::linear_group_f32(lins, x.as<float>(), yp, M, ws.p, ws.n, nullptr);
+  } else {
+    DevBuf ws(w4::linear_group_workspace(lins, M));
+    std::vector<uint16_t*> yp;
+    for (auto& y : ys) yp.push_back(y->as<uint16_t>());
+    w4::linear_group(lins, x.as<uint16_t>(), yp, M, ws.p, ws.n, nullptr);
+  }
+  // o on the attention context
+  DevBuf yo(M * o.n * es);
+  if (f32) {
+    DevBuf ws(o.workspace_f32(M));
+    o.linear_f32(a.as<float>(), yo.as<float>(), M, ws.p, ws.n, nullptr);
+  } else {
+    DevBuf ws(o.workspace(M));
+    o.linear(a.as<uint16_t>(), yo.as<uint16_t>(), M, ws.p, ws.n, nullptr);
+  }
+  // MLP: h = gelu(xff . gate^T) * (xff . up^T), then down fed by h
+  DevBuf h(M * gate.n * es), ymlp(M * down.n * es);
+  if (down.k != gate.n) throw std::runtime_error("down_proj K != gate_proj N");
+  if (f32) {
+    DevBuf ws(w4::gate_up_workspace_f32(gate, M));
+    w4::gate_up_gelu_f32(gate, up, xff.as<float>(), h.as<float>(), M, ws.p, ws.n, nullptr);
+    DevBuf ws2(down.workspace_f32(M));
+    down.linear_f32(h.as<float>(), ymlp.as<float>(), M, ws2.p, ws2.n, nullptr);
+  } else {
+    DevBuf ws(w4::gate_up_workspace(gate, M));
+    w4::gate_up_gelu(gate, up, xff.as<uint16_t>(), h.as<uint16_t>(), M, ws.p, ws.n, nullptr, true);
+    DevBuf ws2(down.workspace(M));
+    down.linear(h.as<uint16_t>(), ymlp.as<uint16_t>(), M, ws2.p, ws2.n, nullptr);
+  }
+  for (size_t i = 0; i < lins.size(); ++i) {
+    const auto b = ys[i]->download();
+    write_file(out + "." + qkv[i] + ".bin", b.data(), b.size());
+  }
+  for (auto* kv : {&yo, &h, &ymlp}) {
+    const auto b = kv->download();
+    const char* tag = kv == &yo ? ".o.bin" : kv == &h ? ".h.bin" : ".mlp.bin";
+    write_file(out + tag, b.data(), b.size());
+  }
+  if (e2b) {
+    const w4::W4Lin pgate = w4::W4Lin::init(store, l + "per_layer_input_gate");
+    const w4::W4Lin pproj = w4::W4Lin::init(store, l + "per_layer_projection");
+    if (pproj.k != pgate.n) throw std::runtime_error("per_layer_projection K != per_layer_input_gate N");
+    const int64_t P = pgate.n;
+    DevBuf h2(M * pgate.k * es), pg(M * P * es), g(M * P * es), yple(M * pproj.n * es);
+    h2.upload(read_file(in + ".h2.bin", h2.n));
+    const auto ple = read_file(in + ".ple.bin", (size_t)(M * P * 4));
+    if (f32) {
+      DevBuf ws(pgate.workspace_f32(M));
+      pgate.linear_f32(h2.as<float>(), pg.as<float>(), M, ws.p, ws.n, nullptr);
+    } else {
+      DevBuf ws(pgate.workspace(M));
+      pgate.linear(h2.as<uint16_t>(), pg.as<uint16_t>(), M, ws.p, ws.n, nullptr);
+    }
+    const auto pgh = pg.download();
+    std::vector<char> gh(g.n);
+    for (int64_t i = 0; i < M * P; ++i) {
+      float v, pi;
+      std::memcpy(&pi, ple.data() + 4 * i, 4);
+      if (f32) std::memcpy(&v, pgh.data() + 4 * i, 4);
+      else {
+        uint16_t b;
+        std::memcpy(&b, pgh.data() + 2 * i, 2);
+        v = bf16_bits_to_float(b);
+      }
+      const float r = gelu_tanh_host(v) * pi;
+      if (f32) std::memcpy(gh.data() + 4 * i, &r, 4);
+      else {
+        const uint16_t b = float_to_bf16_rne(r);
+        std::memcpy(gh.data() + 2 * i, &b, 2);
+      }
+    }
+    g.upload(gh);
+    if (f32) {
+      DevBuf ws(pproj.workspace_f32(M));
+      pproj.linear_f32(g.as<float>(), yple.as<float>(), M, ws.p, ws.n, nullptr);
+    } else {
+      DevBuf ws(pproj.workspace(M));
+      pproj.linear(g.as<uint16_t>(), yple.as<uint16_t>(), M, ws.p, ws.n, nullptr);
+    }
+    write_file(out + ".pg.bin", pgh.data(), pgh.size());
+    write_file(out + ".g.bin", gh.data(), gh.size());
+    const auto b = yple.download();
+    write_file(out + ".ple.bin", b.data(), b.size());
+  }
+  std::printf("{\"layer\": %d, \"model\": \"%s\", \"flow\": \"%s\", \"M\": %lld, \"qkv\": %zu, \"F\": %lld}\n", j,
+              model.c_str(), flow.c_str(), (long long)M, lins.size(), (long long)gate.n);
+  return 0;
+}
+
 int cmd_dequant(int argc, char** argv) {
   if (argc < 5) return usage();
   w4::DeviceStore store(argv[2]);
@@ -274,6 +454,7 @@ int main(int argc, char** argv) {
     if (cmd == "mlp") return cmd_mlp(argc, argv);
     if (cmd == "qkv") return cmd_qkv(argc, argv);
     if (cmd == "head") return cmd_head(argc, argv);
+    if (cmd == "chain") return cmd_chain(argc, argv);
     return usage();
   } catch (const w4::Error& e) {
     std::fprintf(stderr, "w4lin_tool: %s (status %d)\n", e.what(), e.status());

@@ -119,6 +119,9 @@ CASES = [
     (4, 15360, 3840, 32, False, False, False),  # 12B gate/up at M = 4: beyond both GEMV plans -> skinny
     (5, 33, 256, 32, False, False, False),      # 16-row GEMV pair mode
     (8, 6144, 1536, 32, False, True, False),    # 16-row GEMV pair mode: E2B gate/up at M = 8
+    (1, 12288, 1536, 32, False, True, False),   # E2B double-wide gate/up (layers 15-34) at decode
+    (1, 12288, 1536, 32, False, False, True),   # the same, bf16 dots, h bf16 (fam = bf16 flow)
+    (4, 12288, 1536, 32, False, False, True),   # E2B double-wide at M = 4
     (16, 72, 1024, 64, False, False, True),     # 16-row GEMV pair mode, group 64, bf16 dots, h bf16
     (17, 9, 512, 32, False, True, False),       # split-K (skinny form, 2 parts), one real row in the second x block
     (40, 129, 1280, 32, False, True, True),     # split-K (skinny form, 5 parts), bf16 dots

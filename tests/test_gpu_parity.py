@@ -268,6 +268,10 @@ C123 = {  # (K, N)
     # E2B per-layer-embedding linears (engine.zig:659 gate 1536->256, :661 projection 256->1536,
     # :723 per_layer_model_projection 1536->35*256)
     "E2B_ple_gate": (1536, 256), "E2B_ple_proj": (256, 1536), "E2B_plmp": (1536, 8960),
+    # E2B double-wide MLP of the KV-shared layers 15-34 (config.json use_double_wide_mlp,
+    # scripts/57_w4_unpack_fixture.py:74 deq_dn20 [1536, 12288]): gate + up 1536->12288 each
+    # (24576 fused rows) and down 12288->1536
+    "E2B_dw_gateup": (1536, 24576), "E2B_dw_down": (12288, 1536),
 }
 
 
@@ -318,6 +322,28 @@ def test_linear_c4_12b_gateup(M):
     ref32 = o.matmul_f32(x, w)
     check_f32(y[:, rows], x, w, K, ref32)
     check_head_argmax(y[:, rows], ref32, len(rows))
+
+
+C4_LAYER = {"q": (3840, 4096), "kv": (3840, 2048), "o": (4096, 3840), "down": (15360, 3840)}
+
+
+@pytest.mark.parametrize("M", [8, 16, 32, 64])
+@pytest.mark.parametrize("name", list(C4_LAYER))
+def test_linear_c4_12b_layer(name, M):
+    """BASELINE config 3 on the other 12B linears (q, k/v, o, down) at M in {8,16,32,64}:
+    every route these rows take (16-row GEMV, skinny, split-K) against the oracle on
+    every 13th output row, f32 and bf16 outputs."""
+    K, N = C4_LAYER[name]
+    say(f"C4 {name} M={M} K={K} N={N}")
+    _, pk, sc = o.synth_weights(N, K, 1010 + len(name))
+    x = o.synth_x(M, K)
+    rows = np.arange(0, N, 13)
+    w = o.dequant(pk[rows], sc[rows])
+    ref32 = o.matmul_f32(x, w)
+    y = gpu_linear(x, pk, sc, "f32")
+    check_f32(y[:, rows], x, w, K, ref32)
+    _, mag = o.matmul_f64(x, w)
+    check_bf16(gpu_linear(x, pk, sc, "bf16")[:, rows], ref32, mag, K)
 
 
 @pytest.mark.parametrize("M,K,N", [
