@@ -14,8 +14,9 @@ from conftest import ROOT
 
 
 @pytest.mark.skipif(os.environ.get("W4A16_SANITIZER_RUN") == "1", reason="already inside the sanitizer run")
-@pytest.mark.skipif(shutil.which("make") is None or not os.path.exists("/opt/rocm/llvm/bin/clang"),
-                    reason="needs make and ROCm's clang")
+@pytest.mark.skipif(shutil.which("make") is None or not os.path.exists("/opt/rocm/llvm/bin/clang")
+                    or not os.path.exists(os.path.join(ROOT, "tests", "sanitize.sh")),
+                    reason="needs make, ROCm's clang and tests/sanitize.sh")
 def test_cpu_suite_under_asan_ubsan(tmp_path):
     p = subprocess.run(["bash", os.path.join(ROOT, "tests", "sanitize.sh"), str(tmp_path / "tree")],
                        capture_output=True, text=True, timeout=1200)
