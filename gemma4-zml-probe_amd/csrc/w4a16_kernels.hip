@@ -451,6 +451,9 @@ struct GemvArgs {
   int groups_per_row;  // K / group
   int y_f32;
   int steps;           // ceil(K / GSTEP)
+  // gemv_fast_kernel: steps of GSTEP columns per wave within one K segment; the
+  // first wrem waves of a workgroup take wbase + 1 steps, the others wbase
+  int wbase, wrem;
   // gate/up pair mode (gemv_fast_kernel only): pk/sc are gate, pk2/sc2 up,
   // pair_f = F real rows each (0 = plain linear), N = 16 * ceil(F / 8).
   const uint32_t* pk2;
@@ -625,21 +628,32 @@ __global__ void __launch_bounds__(1024) gemv_kernel(GemvArgs a) {
 }
 
 // ---------------------------------------------------------------- GEMV, straight-line variant
-// Same tiling as gemv_kernel, for shapes where K is a multiple of GSTEP and
-// every wave gets exactly NST steps (compile time).  A workgroup covers one
-// 16-row tile; its W = K / (GSTEP * NST) waves split K.
+// Same lane layout as gemv_kernel, for K a multiple of GSTEP * S.  A workgroup covers
+// one tile of R = 16 / S rows of W; its waves split each of the S K segments of the
+// tile's rows into runs of steps (wbase + 1 steps for the first wrem waves, wbase for
+// the others; NST = the longer run, a compile-time bound).
+//
+// K segments (S = 2, M = 1 only): the MFMA's 16 B-operand columns are R rows x S
+// segments of K -- lane r holds row r % R in segment r / R -- and its A operand row r
+// (r < S) holds x of segment r, so D[s][n] for n in segment s is that segment's partial
+// sum; the S partials of a row meet in registers (DPP) before the cross-wave sum.  A
+// tile then spans half as many rows, so a shape with few rows of W gets twice the
+// workgroups and waves.
 //
 // Every load is issued up front, unconditionally (indices clamped) and in a fixed
 // order held by scheduling barriers: this thread's x vectors, then the scales of
 // the wave's NST steps, then its weights step by step.  vmcnt is an in-order
 // per-wave counter, so each step then waits only for its own loads, and x is
-// written to LDS as soon as it lands while the weights are still in flight.  Each
-// lane reads a step's weights and scales at constant offsets from one row pointer
-// (no per-load address arithmetic, so no address registers crowd out the data).
-// XW: each wave stages only its own K range of x (NT planes x M rows x NST * 256
-// columns, XPT vectors per lane) and reads nothing else, so it starts computing
-// without waiting for the other waves; otherwise the workgroup stages all of x
-// (XPT vectors per thread) behind one barrier.
+// written to LDS as soon as it lands while the weights are still in flight.  A wave
+// with a run one step shorter than NST loads its last step twice and skips the
+// duplicate's compute (a wave-uniform branch).  Each lane reads a step's weights and
+// scales at constant offsets from one row pointer (no per-load address arithmetic,
+// so no address registers crowd out the data).
+// XW: each wave stages only its own K ranges of x (NT planes x M rows x S segments x
+// NST * 256 columns, XPT vectors per lane) at their places in the [NT][M][K] LDS
+// image and reads nothing else, so it starts computing without waiting for the other
+// waves; otherwise the workgroup stages all of x (XPT vectors per thread) behind one
+// barrier.
 // Weights are expanded with dequant8_mix.  Tiles past N (odd tile counts) are
 // not written.
 // MR: rows of x the epilogue covers, 4 (M <= 4) or 16 (M <= 16; the MFMA's A
@@ -647,21 +661,28 @@ __global__ void __launch_bounds__(1024) gemv_kernel(GemvArgs a) {
 // PLAIN: one matrix, no gate/up pair (a.pk, a.sc, a.y, a.N only): the kernel then
 // reads none of the group or pair arguments, whose selection the compiler turns into
 // branches with late scalar loads that delay every wave's first weight load.
-template <int NT, int NST, int XPT, bool G32, int MR, bool XW, bool PLAIN = false>
+// S = 2 needs PLAIN, NT = 1, MR = 4, XW and M = 1 (checked on the host).
+template <int NT, int NST, int XPT, bool G32, int MR, bool XW, bool PLAIN = false, int S = 1>
 __global__ void __launch_bounds__(1024) gemv_fast_kernel(GemvArgs a) {
+  static_assert(S == 1 || (S == 2 && PLAIN && NT == 1 && MR == 4 && XW), "K segments: plain M = 1 form only");
+  constexpr int R = 16 / S;  // W rows per tile
   extern __shared__ __attribute__((aligned(16))) uint16_t lds[];
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int nwaves = blockDim.x >> 6;
   const int r = lane & 15;
   const int c = lane >> 4;
-  const int s0 = wave * NST;
+  const int seg = r / R, rr = r % R;  // B column r: row rr of the tile, K segment seg
+  // this wave's run of steps in every segment: [s0, s0 + cnt), cnt = NST or NST - 1
+  const int cnt = a.wbase + (wave < a.wrem ? 1 : 0);
+  const int s0 = wave * a.wbase + min(wave, a.wrem);
   // the block's matrix (a weight group's member, or the single weight) and its tile
   const GroupSel gs = PLAIN ? GroupSel{a.pk, a.sc, a.y, a.N, 0} : group_select(a, (int)blockIdx.x);
   const int pair_f = PLAIN ? 0 : a.pair_f;
   const int N = gs.N;
   const int bt = (int)blockIdx.x - gs.tile0;
   const int K = a.K;
+  const int KS = K / S;  // columns per segment
   const int plane = a.M * K;
 
   // 1. x loads, first (they need nothing but x's address)
@@ -670,13 +691,17 @@ __global__ void __launch_bounds__(1024) gemv_fast_kernel(GemvArgs a) {
   const u32x4* xsrc = reinterpret_cast<const u32x4*>(a.x);
   int xi[XPT];
   if (XW) {
-    // vector v of the wave's share: (plane t, row m) = v / (NST * 32), column vector
-    // s0 * 32 + v % (NST * 32) of that row
-    const int nv = NT * a.M * NST * 32;
+    // vector v of the wave's share: (plane t, row m) = v / (S * NST * 32), then segment
+    // (v / (NST * 32)) % S, then column vector s0 * 32 + u of that segment, u = v % (NST * 32)
+    // clamped to the run's cnt * 32 vectors
+    constexpr int per_seg = NST * 32;
+    const int nv = NT * a.M * S * per_seg;
 #pragma unroll
     for (int i = 0; i < XPT; ++i) {
       const int v = min(lane + 64 * i, nv - 1);
-      xi[i] = (v / (NST * 32)) * (K >> 3) + s0 * 32 + v % (NST * 32);
+      const int pm = v / (S * per_seg), sv_ = (v / per_seg) % S;
+      const int u = min(v % per_seg, cnt * 32 - 1);
+      xi[i] = pm * (K >> 3) + sv_ * (KS >> 3) + s0 * 32 + u;
     }
   } else {
     const int nvec = (NT * plane) >> 3;
@@ -690,24 +715,28 @@ __global__ void __launch_bounds__(1024) gemv_fast_kernel(GemvArgs a) {
 
   // row pointers (pinned in VGPRs as global-memory pointers, so that the compiler
   // forms no address between the loads below)
-  const int tile = min(bt, ((N + 15) >> 4) - 1);
+  const int tile = min(bt, (N + R - 1) / R - 1);
   const uint32_t* pkrow;
   const uint16_t* scrow;
-  weight_row(gs.pk, gs.sc, a.pk2, a.sc2, pair_f, tile * 16 + r, N, K, a.groups_per_row, pkrow, scrow);
-  g_u4* wb = (g_u4*)(reinterpret_cast<const u32x4*>(pkrow) + s0 * 8 + c * 2);
-  g_u32* sb = (g_u32*)(reinterpret_cast<const uint32_t*>(scrow) + s0 * 4 + c);
+  weight_row(gs.pk, gs.sc, a.pk2, a.sc2, pair_f, tile * R + rr, N, K, a.groups_per_row, pkrow, scrow);
+  // first 32-column chunk of this lane's run: segment start, run start, lane group
+  const int cb = seg * (KS >> 5) + s0 * 8 + c * 2;
+  g_u4* wb = (g_u4*)(reinterpret_cast<const u32x4*>(pkrow) + cb);
+  g_u32* sb = (g_u32*)(reinterpret_cast<const uint32_t*>(scrow) + (cb >> 1));
   asm volatile("" : "+v"(wb), "+v"(sb));
   __builtin_amdgcn_sched_barrier(0);
 
-  // 2. scales, then 3. weights, of this wave's NST steps
+  // 2. scales, then 3. weights, of this wave's NST steps (the last one clamped into
+  // the run: a short run loads its last step twice)
+  auto step_of = [&](int i) { return i < NST - 1 ? i : min(i, cnt - 1); };
   uint32_t sv[NST];  // two bf16 scales (low half: the step's first vector)
   if (G32) {
 #pragma unroll
-    for (int i = 0; i < NST; ++i) sv[i] = sb[4 * i];
+    for (int i = 0; i < NST; ++i) sv[i] = sb[4 * step_of(i)];
   } else {
 #pragma unroll
     for (int i = 0; i < NST; ++i) {
-      const int g0 = ((s0 + i) * 4 + c) * VPL;
+      const int g0 = cb + 8 * step_of(i);
       sv[i] = (uint32_t)scrow[g0 / a.group_chunks] | ((uint32_t)scrow[(g0 + 1) / a.group_chunks] << 16);
     }
   }
@@ -715,8 +744,8 @@ __global__ void __launch_bounds__(1024) gemv_fast_kernel(GemvArgs a) {
   u32x4 wv[NST][VPL];
 #pragma unroll
   for (int i = 0; i < NST; ++i) {
-    wv[i][0] = wb[8 * i];
-    wv[i][1] = wb[8 * i + 1];
+    wv[i][0] = wb[8 * step_of(i)];
+    wv[i][1] = wb[8 * step_of(i) + 1];
   }
   __builtin_amdgcn_sched_barrier(0);
 
@@ -729,50 +758,58 @@ __global__ void __launch_bounds__(1024) gemv_fast_kernel(GemvArgs a) {
 
   const MixMasks km = mix_masks();
   floatx4 acc = {0.f, 0.f, 0.f, 0.f};
-  const uint16_t* xrow = lds + min(r, a.M - 1) * K;
+  // A row r: x row r (S = 1, rows past M repeat row M - 1) or x segment r (S = 2)
+  const uint16_t* xrow = S == 1 ? lds + min(r, a.M - 1) * K : lds + (r < S ? r : 0) * KS;
 #pragma unroll
   for (int i = 0; i < NST; ++i) {
+    if (i < NST - 1 || i < cnt) {
 #pragma unroll
-    for (int v = 0; v < VPL; ++v) {
-      const int g = ((s0 + i) * 4 + c) * VPL + v;
-      const MixScale S = mix_scale(v == 0 ? (sv[i] & 0xffffu) : (sv[i] >> 16));
-      const uint16_t* xr = xrow + 32 * g;
-      const uint32_t wj[4] = {wv[i][v][0], wv[i][v][1], wv[i][v][2], wv[i][v][3]};
+      for (int v = 0; v < VPL; ++v) {
+        const MixScale Sc = mix_scale(v == 0 ? (sv[i] & 0xffffu) : (sv[i] >> 16));
+        const uint16_t* xr = xrow + 32 * ((s0 + i) * 8 + c * 2 + v);
+        const uint32_t wj[4] = {wv[i][v][0], wv[i][v][1], wv[i][v][2], wv[i][v][3]};
 #pragma unroll
-      for (int j = 0; j < 4; ++j) {
-        const bf16x8 bb = dequant8_mix(wj[j], S, km);
+        for (int j = 0; j < 4; ++j) {
+          const bf16x8 bb = dequant8_mix(wj[j], Sc, km);
 #pragma unroll
-        for (int t = 0; t < NT; ++t)
-          acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(*reinterpret_cast<const bf16x8*>(xr + t * plane + 8 * j), bb,
-                                                        acc, 0, 0, 0);
+          for (int t = 0; t < NT; ++t)
+            acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(*reinterpret_cast<const bf16x8*>(xr + t * plane + 8 * j),
+                                                          bb, acc, 0, 0, 0);
+        }
       }
     }
   }
 
-  // D: lane (r, c) holds rows m = 4c + i of column r; MR = 4 keeps c == 0 only
+  // D: lane (r, c) holds rows m = 4c + i of column r; MR = 4 keeps c == 0 only.  With
+  // K segments, column r's sum is D[seg][r]: select it, then add the two segments of
+  // row rr (lanes rr and rr + 8, one DPP rotation apart).
   float* red = reinterpret_cast<float*>(lds + NT * plane);  // [waves][MR][16]
-  if (MR == 16 || c == 0) {
+  if (S == 2) {
+    float v = seg == 0 ? acc[0] : acc[1];
+    v += lane_xor8(v);
+    if (c == 0) red[(wave * MR) * 16 + r] = v;
+  } else if (MR == 16 || c == 0) {
 #pragma unroll
     for (int i = 0; i < 4; ++i) red[(wave * MR + (MR == 16 ? 4 * c : 0) + i) * 16 + r] = acc[i];
   }
   __syncthreads();
   for (int t = (int)threadIdx.x; t < 16 * MR; t += (int)blockDim.x) {
-    const int m = t >> 4, rr = t & 15;
-    const int n = bt * 16 + rr;
+    const int m = t >> 4, ro = t & 15;
+    const int n = bt * R + ro;
     if (pair_f) {
-      // gate row rr < 8 of the tile and its up row rr + 8
-      const int f = (bt << 3) + rr;
-      if (rr < 8 && m < a.M && f < pair_f) {
+      // gate row ro < 8 of the tile and its up row ro + 8
+      const int f = (bt << 3) + ro;
+      if (ro < 8 && m < a.M && f < pair_f) {
         float g = 0.f, u = 0.f;
         for (int w = 0; w < nwaves; ++w) {
-          g += red[(w * MR + m) * 16 + rr];
-          u += red[(w * MR + m) * 16 + rr + 8];
+          g += red[(w * MR + m) * 16 + ro];
+          u += red[(w * MR + m) * 16 + ro + 8];
         }
         store_gelu_mul(a.y, a.y_f32, a.bf16_dots, (int64_t)m * pair_f + f, g, u);
       }
-    } else if (m < a.M && n < N) {
+    } else if (m < a.M && ro < R && n < N) {
       float v = 0.f;
-      for (int w = 0; w < nwaves; ++w) v += red[(w * MR + m) * 16 + rr];
+      for (int w = 0; w < nwaves; ++w) v += red[(w * MR + m) * 16 + ro];
       if (a.y_f32) reinterpret_cast<float*>(gs.y)[(int64_t)m * N + n] = v;
       else reinterpret_cast<uint16_t*>(gs.y)[(int64_t)m * N + n] = (uint16_t)f32_to_bf16_rne(v);
     }
@@ -1594,10 +1631,12 @@ hipError_t w4l_fill_zero(void* p, int64_t bytes, hipStream_t st) {
 // ---------------------------------------------------------------- decode GEMV plans
 namespace {
 struct GemvPlan {
-  int nst;    // steps of GSTEP columns per wave
-  int waves;  // waves per workgroup, K / (GSTEP * nst)
+  int nst;    // longest run of GSTEP-column steps per wave (compile-time bound)
+  int waves;  // waves per workgroup; they split each K segment's steps into runs
   int xpt;    // x vectors per lane (per-wave staging) or per thread (workgroup staging)
   bool xw;    // each wave stages only its own K range of x
+  int s;      // K segments per tile (1, or 2: 8-row tiles, M = 1 plain form only)
+  int tiles;  // workgroups (tiles of 16 / s rows)
 };
 // About ten resident waves per SIMD on 256 CUs: a grid of at most this many waves
 // issues every load in its first round.
@@ -1609,21 +1648,58 @@ int pow2_at_least(int64_t v) {
   return p;
 }
 
+bool nst_instanced(int nst) { return (nst >= 1 && nst <= 6) || nst == 8; }
+
+// M = 1, bf16 x: runs of two steps per wave, and where that leaves fewer than
+// 8192 waves (one round of eight waves per SIMD on 256 CUs), more and shorter runs
+// up to 16 waves per workgroup; K in two segments (8-row tiles) where K allows and
+// the caller takes the plain form.  Measured against the uniform-run plans that
+// preceded it (lab sweep over every segment count, waves per workgroup and run
+// length on the 12B and E2B rows, us): 12B gate/up 30720 x 3840 15.0 -> 13.6
+// (runs 2,2,..,2,1 over 8 waves; 3-step runs 14.6, 4-step runs 14.5, more than 8
+// waves 15.8-18.6), down 3840 x 15360 9.9 -> 9.1 (two segments, 16 waves; one
+// segment 9.4, four segments 9.8), q,k,v 8192 x 3840 5.9 -> 5.8, E2B down
+// 1536 x 6144 5.3 -> 4.1, E2B double-wide down 1536 x 12288 7.6 -> 5.2, E2B gate/up
+// 12288 x 1536 4.9 -> 4.8 and 24576 x 1536 6.8 -> 6.3; q 4096 x 3840 and
+// o 3840 x 4096 unchanged (4.5).
+bool gemv_plan_m1(int64_t N, int64_t K, bool allow_s2, GemvPlan* out) {
+  const int s = allow_s2 && K % (2 * w4k::GSTEP) == 0 ? 2 : 1;
+  const int64_t steps = K / (w4k::GSTEP * s), tiles = (N + 16 / s - 1) / (16 / s);
+  if (steps < 1) return false;
+  int64_t nw = (steps + 1) / 2;
+  if (nw > 16) nw = 16;
+  if (tiles * nw < 8192) {
+    int64_t want = (8192 + tiles - 1) / tiles;
+    if (want > 16) want = 16;
+    if (want > steps) want = steps;
+    if (want > nw) nw = want;
+  }
+  const int nst = (int)((steps + nw - 1) / nw);
+  if (!nst_instanced(nst)) return false;
+  const int64_t nv = (int64_t)s * nst * 32;  // x vectors per wave
+  if (nv > 64 * 8) return false;
+  if (K * 2 + nw * 4 * 16 * 4 > 160 * 1024) return false;
+  *out = GemvPlan{nst, (int)nw, pow2_at_least((nv + 63) / 64), true, s, (int)tiles};
+  return true;
+}
+
 // Straight-line GEMV plan for the 4-row (mr = 4, M <= 4) or 16-row (mr = 16,
-// 4 < M <= 16, bf16 x) epilogue.  Per-wave x staging when a wave's share of x,
+// 4 < M <= 16, bf16 x) epilogue.  M = 1 with bf16 x: gemv_plan_m1.  Otherwise
+// per-wave x staging when a wave's share of x,
 // nterms * M * nst * 256 columns, takes at most 8 vectors per lane; then the fewest
 // steps per wave (the most waves, up to 16 per workgroup) whose grid of
-// tiles * waves stays within one round, else the fewest waves.  Measured (us, 12B
-// rows at M = 1, against the next choice): gate/up 1920 tiles, nst 3 15.0 against
-// nst 1 17.4 and nst 5 15.4; down (K = 15360) nst 4 9.6 against nst 5 9.9 and 6
-// 10.7; q, k/v, o nst 1 4.3 / 4.1 / 4.3 against nst 3 (2 for o) 5.1 / 4.9 / 4.6; E2B
-// down nst 2 5.1 against 3 5.3; full-layer o (K = 8192) nst 2 6.8 against 4 7.4.
+// tiles * waves stays within one round, else the fewest waves.
 // Otherwise (f32 x or 16 rows beyond that share) the workgroup stages all of x behind
 // a barrier: the first nst of {5, 2, 4, 1, 3, 6} (4-row form) or the smallest of 1..6
-// (16-row form) with at most 16 waves and 8 vectors per thread.
-bool gemv_plan(int64_t M, int64_t N, int64_t K, int nterms, int mr, GemvPlan* out) {
+// (16-row form) with at most 16 waves and 8 vectors per thread.  Every wave of these
+// plans runs the same number of steps.
+bool gemv_plan(int64_t M, int64_t N, int64_t K, int nterms, int mr, GemvPlan* out, bool allow_s2 = false) {
   if (K % w4k::GSTEP != 0 || M < 1 || N <= 0 || K > (1 << 20)) return false;
   if (mr == 4 ? M > 4 : (M > 16 || nterms != 1)) return false;
+  if (mr == 4 && M == 1 && nterms == 1) {
+    if (allow_s2 && gemv_plan_m1(N, K, true, out)) return true;
+    if (gemv_plan_m1(N, K, false, out)) return true;
+  }
   const int64_t steps = K / w4k::GSTEP, tiles = (N + 15) / 16;
   const int64_t lds_x = (int64_t)nterms * M * K * 2;
   static const int cand[] = {1, 2, 3, 4, 5, 6, 8};
@@ -1637,7 +1713,7 @@ bool gemv_plan(int64_t M, int64_t N, int64_t K, int nterms, int mr, GemvPlan* ou
     if (nv > 64 * 8) continue;
     const int waves = (int)(steps / nst);
     if (lds_x + (int64_t)waves * mr * 16 * 4 > 160 * 1024) continue;
-    best = GemvPlan{nst, waves, pow2_at_least((nv + 63) / 64), true};
+    best = GemvPlan{nst, waves, pow2_at_least((nv + 63) / 64), true, 1, (int)tiles};
     have = true;
     if (tiles * waves <= GEMV_ONE_ROUND_WAVES) break;
   }
@@ -1656,7 +1732,7 @@ bool gemv_plan(int64_t M, int64_t N, int64_t K, int nterms, int mr, GemvPlan* ou
     const int64_t per = (nvec + 64 * waves - 1) / (64 * waves);
     if (per > 8) continue;
     if (lds_x + (int64_t)waves * mr * 16 * 4 > 160 * 1024) continue;
-    *out = GemvPlan{nst, waves, pow2_at_least(per), false};
+    *out = GemvPlan{nst, waves, pow2_at_least(per), false, 1, (int)tiles};
     return true;
   }
   return false;
@@ -1702,13 +1778,15 @@ static hipError_t allow_big_lds(Kern k, size_t lds) {
                              160 * 1024);
 }
 
-template <int NT, int NST, int XPT, int MR, bool XW>
+template <int NT, int NST, int XPT, int MR, bool XW, int S = 1>
 static hipError_t gemv_fast_one(const w4k::GemvArgs& a, dim3 grid, dim3 block, size_t lds, bool g32,
                                 hipStream_t st) {
   // the plain single-matrix form for bf16 x with per-wave staging and the 4-row epilogue
-  const bool plain = NT == 1 && MR == 4 && XW && a.nmat <= 1 && a.pair_f == 0;
-  auto k = plain ? (g32 ? w4k::gemv_fast_kernel<NT, NST, XPT, true, MR, XW, NT == 1 && MR == 4 && XW>
-                        : w4k::gemv_fast_kernel<NT, NST, XPT, false, MR, XW, NT == 1 && MR == 4 && XW>)
+  constexpr bool PL = NT == 1 && MR == 4 && XW;
+  const bool plain = PL && a.nmat <= 1 && a.pair_f == 0;
+  if (S != 1 && !(plain && a.M == 1)) return hipErrorInvalidValue;
+  auto k = plain ? (g32 ? w4k::gemv_fast_kernel<NT, NST, XPT, true, MR, XW, PL, (PL ? S : 1)>
+                        : w4k::gemv_fast_kernel<NT, NST, XPT, false, MR, XW, PL, (PL ? S : 1)>)
                  : (g32 ? w4k::gemv_fast_kernel<NT, NST, XPT, true, MR, XW> : w4k::gemv_fast_kernel<NT, NST, XPT, false, MR, XW>);
   hipError_t e = allow_big_lds(k, lds);
   if (e != hipSuccess) return e;
@@ -1719,18 +1797,25 @@ static hipError_t gemv_fast_one(const w4k::GemvArgs& a, dim3 grid, dim3 block, s
 // Launch of gemv_fast_kernel for a filled GemvArgs and a plan (instances: bf16 x with
 // per-wave staging, steps 1..6 and 8; f32 x per wave up to 5 steps, or the workgroup
 // form; the 16-row epilogue per wave at 1 step, or the workgroup form).
-static hipError_t gemv_fast_launch(const w4k::GemvArgs& a, int nterms, int mr, const GemvPlan& p, int nblocks,
+static hipError_t gemv_fast_launch(const w4k::GemvArgs& a0, int nterms, int mr, const GemvPlan& p, int nblocks,
                                    bool g32, hipStream_t st) {
+  // runs of steps: every K segment's steps over the plan's waves (at least one step each)
+  w4k::GemvArgs a = a0;
+  const int steps = a.K / (w4k::GSTEP * p.s);
+  if (p.waves < 1 || p.waves > steps || (steps + p.waves - 1) / p.waves != p.nst) return hipErrorInvalidValue;
+  a.wbase = steps / p.waves;
+  a.wrem = steps % p.waves;
   const size_t lds = (size_t)nterms * a.M * a.K * 2 + (size_t)p.waves * mr * 16 * 4;
   const dim3 grid((unsigned)nblocks), block(64 * p.waves);
-#define W4_GF(NT_, NST_, MR_, XW_)                                                          \
-  switch (p.xpt) {                                                                          \
-    case 1: return gemv_fast_one<NT_, NST_, 1, MR_, XW_>(a, grid, block, lds, g32, st);     \
-    case 2: return gemv_fast_one<NT_, NST_, 2, MR_, XW_>(a, grid, block, lds, g32, st);     \
-    case 4: return gemv_fast_one<NT_, NST_, 4, MR_, XW_>(a, grid, block, lds, g32, st);     \
-    case 8: return gemv_fast_one<NT_, NST_, 8, MR_, XW_>(a, grid, block, lds, g32, st);     \
-    default: return hipErrorInvalidValue;                                                   \
+#define W4_GFS(NT_, NST_, MR_, XW_, S_)                                                           \
+  switch (p.xpt) {                                                                                \
+    case 1: return gemv_fast_one<NT_, NST_, 1, MR_, XW_, S_>(a, grid, block, lds, g32, st);       \
+    case 2: return gemv_fast_one<NT_, NST_, 2, MR_, XW_, S_>(a, grid, block, lds, g32, st);       \
+    case 4: return gemv_fast_one<NT_, NST_, 4, MR_, XW_, S_>(a, grid, block, lds, g32, st);       \
+    case 8: return gemv_fast_one<NT_, NST_, 8, MR_, XW_, S_>(a, grid, block, lds, g32, st);       \
+    default: return hipErrorInvalidValue;                                                         \
   }
+#define W4_GF(NT_, NST_, MR_, XW_) W4_GFS(NT_, NST_, MR_, XW_, 1)
 #define W4_GF6(NT_, MR_, XW_)                     \
   switch (p.nst) {                                \
     case 1: W4_GF(NT_, 1, MR_, XW_)               \
@@ -1741,6 +1826,19 @@ static hipError_t gemv_fast_launch(const w4k::GemvArgs& a, int nterms, int mr, c
     case 6: W4_GF(NT_, 6, MR_, XW_)               \
     default: return hipErrorInvalidValue;         \
   }
+  if (mr == 4 && nterms == 1 && p.xw && p.s == 2) {
+    switch (p.nst) {
+      case 1: W4_GFS(1, 1, 4, true, 2)
+      case 2: W4_GFS(1, 2, 4, true, 2)
+      case 3: W4_GFS(1, 3, 4, true, 2)
+      case 4: W4_GFS(1, 4, 4, true, 2)
+      case 5: W4_GFS(1, 5, 4, true, 2)
+      case 6: W4_GFS(1, 6, 4, true, 2)
+      case 8: W4_GFS(1, 8, 4, true, 2)
+      default: return hipErrorInvalidValue;
+    }
+  }
+  if (p.s != 1) return hipErrorInvalidValue;
   if (mr == 4 && nterms == 1 && p.xw) {
     switch (p.nst) {
       case 1: W4_GF(1, 1, 4, true)
@@ -1771,6 +1869,7 @@ static hipError_t gemv_fast_launch(const w4k::GemvArgs& a, int nterms, int mr, c
   if (mr == 16 && nterms == 1) W4_GF6(1, 16, false)
 #undef W4_GF6
 #undef W4_GF
+#undef W4_GFS
   return hipErrorInvalidValue;
 }
 
@@ -1779,9 +1878,10 @@ hipError_t w4l_gemv(const uint16_t* x_planes, int nterms, const int32_t* pk, con
                     hipStream_t st, const W4Pair* pair) {
   if (pair) N = 16 * ((pair->F + 7) / 8);
   // the 4-row form where its plan holds, else the 16-row form (M <= 16, bf16 x)
+  // K segments (8-row tiles) only for the plain single-matrix form
   GemvPlan p;
   int mr = 4;
-  if (!(w4l_gemv_ok(M, K, nterms) && gemv_plan(M, N, K, nterms, 4, &p))) {
+  if (!(w4l_gemv_ok(M, K, nterms) && gemv_plan(M, N, K, nterms, 4, &p, pair == nullptr))) {
     mr = 16;
     if (!gemv_plan(M, N, K, nterms, 16, &p)) mr = 0;
   }
@@ -1804,7 +1904,7 @@ hipError_t w4l_gemv(const uint16_t* x_planes, int nterms, const int32_t* pk, con
   }
   if (mr) {
     a.steps = (int)(K / w4k::GSTEP);
-    return gemv_fast_launch(a, nterms, mr, p, (int)((N + 15) / 16), group == 32, st);
+    return gemv_fast_launch(a, nterms, mr, p, p.tiles, group == 32, st);
   }
   if (pair) return hipErrorInvalidValue;
   a.steps = (int)((K + w4k::GSTEP - 1) / w4k::GSTEP);

@@ -653,6 +653,51 @@ def test_gemv_tile_counts(N):
     check_bf16(yb, ref32, mag, K)
 
 
+@pytest.mark.parametrize("N,K,group", [
+    # two K segments (8-row tiles, K % 512 == 0): one step per segment, ragged N, 5 and
+    # 15 steps per segment over as many waves, 30 over 16 waves (runs 2,..,2,1,1),
+    # groups 64 / 128
+    (1, 512, 32), (7, 512, 32), (9, 1024, 32), (1001, 2560, 32), (300, 7680, 32),
+    (3840, 15360, 32), (200, 1536, 64), (136, 3072, 128),
+    # one K segment, uneven runs: 17 steps over 16 waves (one run of 2), 15 steps over
+    # 8 waves (runs 2,..,2,1) with a ragged last tile
+    (2000, 4352, 32), (16390, 3840, 32)])
+def test_decode_gemv_k_segments_and_uneven_runs(N, K, group):
+    """M = 1 decode GEMV plans: K in two segments where K % 512 == 0 (the B operand's
+    16 columns are 8 rows x 2 halves of K, A row s carries x of half s), and runs of
+    steps that differ by one between the waves of a workgroup (a short run loads its
+    last step twice and computes it once).  Against the oracle, f32 and bf16 out."""
+    say(f"decode segments / uneven runs N={N} K={K} group={group}")
+    _, pk, sc = o.synth_weights(N, K, 62, group)
+    x = o.synth_x(1, K, 63)
+    w = o.dequant(pk, sc, group)
+    ref32 = o.matmul_f32(x, w)
+    y = gpu_linear(x, pk, sc, "f32", group=group)
+    check_f32(y, x, w, K, ref32)
+    yb = gpu_linear(x, pk, sc, "bf16", group=group)
+    _, mag = o.matmul_f64(x, w)
+    check_bf16(yb, ref32, mag, K)
+
+
+def test_decode_gemv_segments_one_hot():
+    """M = 1, K = 512: two K segments of one step each.  A one-hot x at column k selects
+    weight k of every row, so y must reproduce the bf16 weight exactly, for columns in
+    either segment and at both ends of each (pins which half of K each A row and each
+    B column carries)."""
+    N, K = 4096, 512
+    _, pk, sc = o.synth_weights(N, K, 61)
+    w = o.bf16_to_f32(o.dequant(pk, sc))
+    pkd, scd = dev(pk), dev_u16(sc)
+    for k in (0, 7, 200, 255, 256, 263, 400, 511):
+        x = np.zeros((1, K), dtype=np.uint16)
+        x[0, k] = 0x3F80
+        y = w4a16.linear(dev_u16(x), pkd, scd, out_dtype=torch.float32)
+        torch.cuda.synchronize()
+        y = y.cpu().numpy()[0]
+        bad = np.flatnonzero(y != w[:, k])
+        assert bad.size == 0, (k, bad[:5].tolist())
+
+
 @pytest.mark.parametrize("M,N,K", [(17, 200, 640), (32, 130, 640), (48, 2048, 1344), (64, 300, 960)])
 def test_prefill_kernel_small_m(M, N, K):
     """The 32x32 kernel with 32 or 64 rows of x per workgroup over K parts (the split-K
