@@ -850,14 +850,19 @@ struct SkinnyArgs {
   float* part;
 };
 
-constexpr int SK_P = 4;  // weight prefetch depth (chunks); even, for the two-slot x ring (8: 8-10 % slower)
+// Weight prefetch depth (chunks); even, for the two-slot x ring.  Four x blocks (MT = 4,
+// M = 49..64) take 2: with a wave waiting on its x staging (an in-order vmcnt wait that
+// also covers every earlier weight load) the deeper ring only adds registers (12B gate/up
+// at M = 64: 30.1 -> 28.9 us in the lab; 8 slots were 8-10 % slower at every M).
+template <int MT>
+constexpr int sk_prefetch() { return MT == 4 ? 2 : 4; }
 
 // NW waves of 16 W rows per workgroup (4 or 8): 8 halves the x traffic from L2
 // (x is staged once per 16 * NW rows of W).
 template <int MT, bool G32, int NW = 4>
 __global__ void __launch_bounds__(64 * NW) skinny_kernel(SkinnyArgs a) {
   constexpr int NTH = 64 * NW;
-  constexpr int P = SK_P;
+  constexpr int P = sk_prefetch<MT>();
   // x rows of 256 halves as 4 groups of 64 (one lane group c each), every group padded
   // to 72 halves and every row to 304: the A-fragment reads (16 rows, lane groups
   // 144 B apart) are then free of LDS bank conflicts (measured on gfx950: a 16-byte
