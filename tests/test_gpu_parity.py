@@ -166,17 +166,18 @@ def test_w2_u1b_dequant_shape_families(name):
 
 def test_linear_one_hot_reproduces_dequant_exactly():
     """One-hot rows of x select single weights: y must equal the bf16 weight
-    exactly.  Over every bf16 scale pattern in the fused kernel's exact range
-    this pins its in-register dequant to dequantW4's rounding.  Stated range:
-    2^-126 <= |s| < 2^120.  Below it v_dot2_f32_bf16 flushes the subnormal scale
-    (weights of magnitude <= 8 * 2^-126 come out as 0); above it the
-    intermediate (128 + n) * s of the in-register dequant overflows fp32.
-    Checkpoint scales are max_abs / 7.5 of bf16 weights, around 2^-20..2^-3."""
+    exactly.  Over every bf16 scale pattern in the fused kernels' exact range
+    this pins the in-register dequant of the M > 4 kernels (32 rows of x: the
+    skinny kernel's f16 form) to dequantW4's rounding.  Stated range:
+    2^-126 <= |s| < 2^117.  Subnormal scales may be flushed (weights of magnitude
+    <= 8 * 2^-126 come out as 0); from 2^117 the intermediate (1024 + n) * s
+    overflows fp32.  Checkpoint scales are max_abs / 7.5 of bf16 weights, around
+    2^-20..2^-3."""
     say("linear one-hot over all finite scale patterns")
     q = np.tile(np.arange(-8, 8, dtype=np.int8), 2)[None].repeat(65536, 0)
     sc = np.arange(65536, dtype=np.uint32).astype(np.uint16)[:, None].copy()
     expo = (sc[:, 0] >> 7) & 0xFF                     # biased exponent
-    in_range = (expo >= 1) & (expo < 127 + 120)
+    in_range = (expo >= 1) & (expo < 127 + 117)
     subnormal = (expo == 0) & ((sc[:, 0] & 0x7F) != 0)
     assert subnormal.sum() == 254
     sc[~(in_range | subnormal), 0] = 0                # drop huge / non-finite scales
