@@ -1660,20 +1660,22 @@ int pow2_at_least(int64_t v) {
 
 bool nst_instanced(int nst) { return (nst >= 1 && nst <= 6) || nst == 8; }
 
-// M = 1, bf16 x: runs of two steps per wave, and where that leaves fewer than
-// 8192 waves (one round of eight waves per SIMD on 256 CUs), more and shorter runs
-// up to 16 waves per workgroup; K in two segments (8-row tiles) where K allows and
-// the caller takes the plain form.  Measured against the uniform-run plans that
-// preceded it (lab sweep over every segment count, waves per workgroup and run
-// length on the 12B and E2B rows, us): 12B gate/up 30720 x 3840 15.0 -> 13.6
-// (runs 2,2,..,2,1 over 8 waves; 3-step runs 14.6, 4-step runs 14.5, more than 8
-// waves 15.8-18.6), down 3840 x 15360 9.9 -> 9.1 (two segments, 16 waves; one
-// segment 9.4, four segments 9.8), q,k,v 8192 x 3840 5.9 -> 5.8, E2B down
+// M <= 4 (the 4-row epilogue), bf16 or f32 x: runs of two steps per wave, and where
+// that leaves fewer than 8192 waves (one round of eight waves per SIMD on 256 CUs),
+// more and shorter runs up to 16 waves per workgroup; K in two segments (8-row tiles)
+// where M = 1, x is bf16, K allows and the caller takes the plain form.  Measured
+// against the uniform-run plans that preceded it (lab sweep over every segment count,
+// waves per workgroup and run length on the 12B and E2B rows at M = 1, us): 12B gate/up
+// 30720 x 3840 15.0 -> 13.6 (runs 2,..,2,1 over 8 waves; 3-step runs 14.6, 4-step runs
+// 14.5, more than 8 waves 15.8-18.6), down 3840 x 15360 9.9 -> 9.1 (two segments, 16
+// waves; one segment 9.4, four segments 9.8), q,k,v 8192 x 3840 5.9 -> 5.8, E2B down
 // 1536 x 6144 5.3 -> 4.1, E2B double-wide down 1536 x 12288 7.6 -> 5.2, E2B gate/up
-// 12288 x 1536 4.9 -> 4.8 and 24576 x 1536 6.8 -> 6.3; q 4096 x 3840 and
-// o 3840 x 4096 unchanged (4.5).
-bool gemv_plan_m1(int64_t N, int64_t K, bool allow_s2, GemvPlan* out) {
-  const int s = allow_s2 && K % (2 * w4k::GSTEP) == 0 ? 2 : 1;
+// 12288 x 1536 4.9 -> 4.8 and 24576 x 1536 6.8 -> 6.3; q 4096 x 3840 and o 3840 x 4096
+// unchanged (4.5).  A/B of the product on one box: 12B gate/up at M = 2 / 4 16.1 / 19.3 ->
+// 15.0 / 17.7, with f32 x at M = 1 / 2 23.1 / 27.1 -> 20.4 / 24.2; down, q and E2B rows
+// at M = 2..4 unchanged.
+bool gemv_plan_runs(int64_t M, int64_t N, int64_t K, int nterms, bool allow_s2, GemvPlan* out) {
+  const int s = allow_s2 && M == 1 && nterms == 1 && K % (2 * w4k::GSTEP) == 0 ? 2 : 1;
   const int64_t steps = K / (w4k::GSTEP * s), tiles = (N + 16 / s - 1) / (16 / s);
   if (steps < 1) return false;
   int64_t nw = (steps + 1) / 2;
@@ -1685,16 +1687,16 @@ bool gemv_plan_m1(int64_t N, int64_t K, bool allow_s2, GemvPlan* out) {
     if (want > nw) nw = want;
   }
   const int nst = (int)((steps + nw - 1) / nw);
-  if (!nst_instanced(nst)) return false;
-  const int64_t nv = (int64_t)s * nst * 32;  // x vectors per wave
+  if (!nst_instanced(nst) || (nterms == 3 && nst > 5)) return false;
+  const int64_t nv = (int64_t)nterms * M * s * nst * 32;  // x vectors per wave
   if (nv > 64 * 8) return false;
-  if (K * 2 + nw * 4 * 16 * 4 > 160 * 1024) return false;
+  if ((int64_t)nterms * M * K * 2 + nw * 4 * 16 * 4 > 160 * 1024) return false;
   *out = GemvPlan{nst, (int)nw, pow2_at_least((nv + 63) / 64), true, s, (int)tiles};
   return true;
 }
 
 // Straight-line GEMV plan for the 4-row (mr = 4, M <= 4) or 16-row (mr = 16,
-// 4 < M <= 16, bf16 x) epilogue.  M = 1 with bf16 x: gemv_plan_m1.  Otherwise
+// 4 < M <= 16, bf16 x) epilogue.  The 4-row form: gemv_plan_runs where it holds.  Otherwise
 // per-wave x staging when a wave's share of x,
 // nterms * M * nst * 256 columns, takes at most 8 vectors per lane; then the fewest
 // steps per wave (the most waves, up to 16 per workgroup) whose grid of
@@ -1706,9 +1708,9 @@ bool gemv_plan_m1(int64_t N, int64_t K, bool allow_s2, GemvPlan* out) {
 bool gemv_plan(int64_t M, int64_t N, int64_t K, int nterms, int mr, GemvPlan* out, bool allow_s2 = false) {
   if (K % w4k::GSTEP != 0 || M < 1 || N <= 0 || K > (1 << 20)) return false;
   if (mr == 4 ? M > 4 : (M > 16 || nterms != 1)) return false;
-  if (mr == 4 && M == 1 && nterms == 1) {
-    if (allow_s2 && gemv_plan_m1(N, K, true, out)) return true;
-    if (gemv_plan_m1(N, K, false, out)) return true;
+  if (mr == 4) {
+    if (allow_s2 && gemv_plan_runs(M, N, K, nterms, true, out)) return true;
+    if (gemv_plan_runs(M, N, K, nterms, false, out)) return true;
   }
   const int64_t steps = K / w4k::GSTEP, tiles = (N + 15) / 16;
   const int64_t lds_x = (int64_t)nterms * M * K * 2;
