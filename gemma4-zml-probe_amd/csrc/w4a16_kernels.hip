@@ -1673,8 +1673,11 @@ bool nst_instanced(int nst) { return (nst >= 1 && nst <= 6) || nst == 8; }
 // 12288 x 1536 4.9 -> 4.8 and 24576 x 1536 6.8 -> 6.3; q 4096 x 3840 and o 3840 x 4096
 // unchanged (4.5).  A/B of the product on one box: 12B gate/up at M = 2 / 4 16.1 / 19.3 ->
 // 15.0 / 17.7, with f32 x at M = 1 / 2 23.1 / 27.1 -> 20.4 / 24.2; down, q and E2B rows
-// at M = 2..4 unchanged.
-bool gemv_plan_runs(int64_t M, int64_t N, int64_t K, int nterms, bool allow_s2, GemvPlan* out) {
+// at M = 2..4 unchanged.  The 16-row form (mr = 16, bf16 x, runs of at most 2 steps)
+// uses the same rule: E2B down at M = 8 7.7 -> 7.2 us, the other rows it serves unchanged.
+// (Through this form at M = 5..16, 12B gate/up measured 13-110 % slower than the skinny
+// kernel: every 16-row tile re-reads x from L2; the 40 MiB rule of w4l_gemv16_ok holds.)
+bool gemv_plan_runs(int64_t M, int64_t N, int64_t K, int nterms, int mr, bool allow_s2, GemvPlan* out) {
   const int s = allow_s2 && M == 1 && nterms == 1 && K % (2 * w4k::GSTEP) == 0 ? 2 : 1;
   const int64_t steps = K / (w4k::GSTEP * s), tiles = (N + 16 / s - 1) / (16 / s);
   if (steps < 1) return false;
@@ -1687,10 +1690,10 @@ bool gemv_plan_runs(int64_t M, int64_t N, int64_t K, int nterms, bool allow_s2, 
     if (want > nw) nw = want;
   }
   const int nst = (int)((steps + nw - 1) / nw);
-  if (!nst_instanced(nst) || (nterms == 3 && nst > 5)) return false;
+  if (!nst_instanced(nst) || (nterms == 3 && nst > 5) || (mr == 16 && nst > 2)) return false;
   const int64_t nv = (int64_t)nterms * M * s * nst * 32;  // x vectors per wave
   if (nv > 64 * 8) return false;
-  if ((int64_t)nterms * M * K * 2 + nw * 4 * 16 * 4 > 160 * 1024) return false;
+  if ((int64_t)nterms * M * K * 2 + nw * mr * 16 * 4 > 160 * 1024) return false;
   *out = GemvPlan{nst, (int)nw, pow2_at_least((nv + 63) / 64), true, s, (int)tiles};
   return true;
 }
@@ -1708,9 +1711,9 @@ bool gemv_plan_runs(int64_t M, int64_t N, int64_t K, int nterms, bool allow_s2, 
 bool gemv_plan(int64_t M, int64_t N, int64_t K, int nterms, int mr, GemvPlan* out, bool allow_s2 = false) {
   if (K % w4k::GSTEP != 0 || M < 1 || N <= 0 || K > (1 << 20)) return false;
   if (mr == 4 ? M > 4 : (M > 16 || nterms != 1)) return false;
-  if (mr == 4) {
-    if (allow_s2 && gemv_plan_runs(M, N, K, nterms, true, out)) return true;
-    if (gemv_plan_runs(M, N, K, nterms, false, out)) return true;
+  if (mr == 4 || nterms == 1) {
+    if (allow_s2 && gemv_plan_runs(M, N, K, nterms, mr, true, out)) return true;
+    if (gemv_plan_runs(M, N, K, nterms, mr, false, out)) return true;
   }
   const int64_t steps = K / w4k::GSTEP, tiles = (N + 15) / 16;
   const int64_t lds_x = (int64_t)nterms * M * K * 2;
@@ -1875,8 +1878,11 @@ static hipError_t gemv_fast_launch(const w4k::GemvArgs& a0, int nterms, int mr, 
   }
   if (mr == 4 && nterms == 3) W4_GF6(3, 4, false)
   if (mr == 16 && nterms == 1 && p.xw) {
-    if (p.nst != 1) return hipErrorInvalidValue;
-    W4_GF(1, 1, 16, true)
+    switch (p.nst) {
+      case 1: W4_GF(1, 1, 16, true)
+      case 2: W4_GF(1, 2, 16, true)
+      default: return hipErrorInvalidValue;
+    }
   }
   if (mr == 16 && nterms == 1) W4_GF6(1, 16, false)
 #undef W4_GF6
