@@ -350,6 +350,32 @@ def time_lm_head(torch, w4a16, o, M, V, K, k):
             "hbm_frac": nbytes / t / 1e9 / PEAK_HBM_GBS}
 
 
+def time_dequant(torch, w4a16, N, K):
+    """Average durations of one w4a16_dequant call (bf16 [N, K] out) and one
+    w4a16_unpack call (int8 [N, K] out), each a HIP graph of back-to-back calls
+    rotating over packed weight sets larger than the MALL."""
+    nsets = max(2, -(-ROTATE_BYTES // (N * K // 2 + N * K // 16)))
+    sets = [make_set(torch, None, K, N, 7500 + i) for i in range(nsets)]
+    w = torch.empty((N, K), dtype=torch.bfloat16, device="cuda")
+    q = torch.empty((N, K), dtype=torch.int8, device="cuda")
+    launches = nsets * max(1, -(-20 // nsets))
+    out = {"N": N, "K": K, "launches": launches}
+    for name, fn, nbytes in (
+            ("dequant", lambda pk, sc: w4a16.dequantW4(pk, sc, out=w), N * K // 2 + N * K // 16 + 2 * N * K),
+            ("unpack", lambda pk, sc: w4a16.unpackW4(pk, out=q), N * K // 2 + N * K)):
+        def run(fn=fn):
+            for i in range(launches):
+                fn(*sets[i % nsets])
+        g = graph_of(torch, run)
+        t = time_graph(torch, g, 3) / (3 * launches)
+        del g
+        out[name] = {"bytes_per_call": nbytes, "avg_call_us": round(t * 1e6, 3), "GBps": round(nbytes / t / 1e9, 1),
+                     "hbm_frac": round(nbytes / t / 1e9 / PEAK_HBM_GBS, 4)}
+    del sets
+    torch.cuda.empty_cache()
+    return out
+
+
 def main() -> int:
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -372,6 +398,9 @@ def main() -> int:
     ap.add_argument("--lm-head", type=str, default=None,
                     help="M,V,K,k: time only the lm_head call (logits, softcap 30, top-k); the workload of "
                          "its kernel traces")
+    ap.add_argument("--dequant", type=str, default=None,
+                    help="N,K: time only w4a16_dequant and w4a16_unpack on [N, K] weights; the workload of "
+                         "their kernel traces")
     ap.add_argument("--no-unfused", action="store_true",
                     help="with --gate-up: time only the fused call (the workload of its kernel traces)")
     ap.add_argument("--copy-calibration", action="store_true",
@@ -423,6 +452,11 @@ def main() -> int:
                           "unfused_us": round(r["unfused_us"], 3) if "unfused_us" in r else None,
                           "GBps": round(r["GBps"], 1), "TFLOPs": round(r["TFLOPs"], 2),
                           "launches_per_replay": r["launches"]}), flush=True)
+        return 0
+
+    if args.dequant:
+        qN, qK = (int(v) for v in args.dequant.split(","))
+        print(json.dumps(time_dequant(torch, w4a16, qN, qK)), flush=True)
         return 0
 
     if args.lm_head:

@@ -223,66 +223,65 @@ __device__ __forceinline__ bf16x8 dequant8_mix(uint32_t w, const MixScale& S, co
   return __builtin_bit_cast(bf16x8, r);
 }
 
-// ================================================================ unpack
-// Flat over words: word i -> q[8i .. 8i+7].  Main part in 4-word chunks.
+// ================================================================ unpack, dequant
+// Flat over packed words: word i holds weights 8i .. 8i+7 of the [N, K] matrix (rows
+// are K/8 whole words).  One word per lane per unit, U units per thread 256 words
+// apart, so every load instruction reads 256 consecutive words and every store writes
+// one contiguous block (2 KiB of int8 q, 4 KiB of bf16 w per 256 lanes); U = 4 keeps
+// four words in flight per lane on large matrices.  (The first form, one thread per
+// 32-column chunk with 16-byte stores 64 bytes apart and a 64-bit division per chunk,
+// ran dequant at 3.4-3.7 TB/s on 12B-sized matrices; this form at 5.8-6.1.)
+template <int U>
 __global__ void __launch_bounds__(256) unpack_kernel(const uint32_t* __restrict__ pk,
                                                      int8_t* __restrict__ q, int64_t nwords) {
-  const int64_t nchunks = nwords >> 2;
-  const int64_t stride = (int64_t)gridDim.x * blockDim.x;
-  for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < nchunks; i += stride) {
-    const uint4 w = reinterpret_cast<const uint4*>(pk)[i];
-    const uint32_t ws[4] = {w.x, w.y, w.z, w.w};
-    uint32_t out[8];
+  const int64_t base = (int64_t)blockIdx.x * (256 * U) + threadIdx.x;
+  uint32_t wd[U];
 #pragma unroll
-    for (int d = 0; d < 4; ++d) {
-      uint32_t lo = 0, hi = 0;
+  for (int u = 0; u < U; ++u) wd[u] = pk[min(base + 256 * u, nwords - 1)];
 #pragma unroll
-      for (int j = 0; j < 4; ++j) {
-        lo |= (uint32_t)(uint8_t)((int)((ws[d] >> (4 * j)) & 0xFu) - 8) << (8 * j);
-        hi |= (uint32_t)(uint8_t)((int)((ws[d] >> (4 * j + 16)) & 0xFu) - 8) << (8 * j);
-      }
-      out[2 * d] = lo;
-      out[2 * d + 1] = hi;
+  for (int u = 0; u < U; ++u) {
+    const int64_t i = base + 256 * u;
+    // n - 8 is the nibble n ^ 8 read as a signed 4-bit number
+    const uint32_t t = wd[u] ^ 0x88888888u;
+    uint32_t lo = 0, hi = 0;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      lo |= ((uint32_t)((int32_t)(t << (28 - 4 * j)) >> 28) & 0xFFu) << (8 * j);
+      hi |= ((uint32_t)((int32_t)(t << (12 - 4 * j)) >> 28) & 0xFFu) << (8 * j);
     }
-    uint4* dst = reinterpret_cast<uint4*>(q) + 2 * i;
-    dst[0] = make_uint4(out[0], out[1], out[2], out[3]);
-    dst[1] = make_uint4(out[4], out[5], out[6], out[7]);
-  }
-  // tail words (nwords % 4)
-  const int64_t t = (nchunks << 2) + (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
-  if (t < nwords && t >= (nchunks << 2)) {
-    const uint32_t w = pk[t];
-    for (int j = 0; j < 8; ++j) q[8 * t + j] = (int8_t)((int)((w >> (4 * j)) & 0xFu) - 8);
+    if (i < nwords) reinterpret_cast<uint2*>(q)[i] = make_uint2(lo, hi);
   }
 }
 
-// ================================================================ dequant
-// One thread per 32-column chunk of a row (K % 32 == 0, group % 32 == 0: the
-// chunk lies inside one scale group).  Bit-exact RNE_bf16(float(q) * s).
+// Bit-exact RNE_bf16(float(q) * s).  Word i's scale is sc[i / (group / 8)] for every
+// row: K % group == 0 starts each row on a group boundary, so the flat word index
+// divided by the words per group is the flat scale index (a shift when group / 8 is a
+// power of two, shift < 0 otherwise).
+template <int U>
 __global__ void __launch_bounds__(256) dequant_kernel(const uint32_t* __restrict__ pk,
                                                       const uint16_t* __restrict__ sc,
-                                                      uint16_t* __restrict__ w, int64_t nchunks,
-                                                      int64_t chunks_per_row, int64_t groups_per_row,
-                                                      int32_t chunks_per_group) {
-  const int64_t stride = (int64_t)gridDim.x * blockDim.x;
-  for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < nchunks; i += stride) {
-    const int64_t n = i / chunks_per_row;
-    const int64_t c = i - n * chunks_per_row;
-    const float s = bf16_bits_to_f32(sc[n * groups_per_row + c / chunks_per_group]);
-    const uint4 v = reinterpret_cast<const uint4*>(pk)[i];
-    const uint32_t ws[4] = {v.x, v.y, v.z, v.w};
-    uint32_t o[16];
+                                                      uint16_t* __restrict__ w, int64_t nwords,
+                                                      int64_t words_per_group, int shift) {
+  const int64_t base = (int64_t)blockIdx.x * (256 * U) + threadIdx.x;
+  uint32_t wd[U];
+  float s[U];
 #pragma unroll
-    for (int d = 0; d < 4; ++d)
+  for (int u = 0; u < U; ++u) {
+    const int64_t i = min(base + 256 * u, nwords - 1);
+    wd[u] = pk[i];
+    s[u] = bf16_bits_to_f32(sc[shift >= 0 ? (i >> shift) : (i / words_per_group)]);
+  }
 #pragma unroll
-      for (int j = 0; j < 4; ++j) {
-        const float a = (float)((int)((ws[d] >> (8 * j)) & 0xFu) - 8) * s;
-        const float b = (float)((int)((ws[d] >> (8 * j + 4)) & 0xFu) - 8) * s;
-        o[4 * d + j] = f32_to_bf16_rne(a) | (f32_to_bf16_rne(b) << 16);
-      }
-    uint4* dst = reinterpret_cast<uint4*>(w) + 4 * i;
+  for (int u = 0; u < U; ++u) {
+    const int64_t i = base + 256 * u;
+    uint32_t o[4];
 #pragma unroll
-    for (int e = 0; e < 4; ++e) dst[e] = make_uint4(o[4 * e], o[4 * e + 1], o[4 * e + 2], o[4 * e + 3]);
+    for (int j = 0; j < 4; ++j) {
+      const float a = (float)((int)((wd[u] >> (8 * j)) & 0xFu) - 8) * s[u];
+      const float b = (float)((int)((wd[u] >> (8 * j + 4)) & 0xFu) - 8) * s[u];
+      o[j] = f32_to_bf16_rne(a) | (f32_to_bf16_rne(b) << 16);
+    }
+    if (i < nwords) reinterpret_cast<uint4*>(w)[i] = make_uint4(o[0], o[1], o[2], o[3]);
   }
 }
 
@@ -1605,21 +1604,34 @@ int grid_for(int64_t work, int block) {
 }
 }  // namespace
 
+// Four words per thread once there are enough words for ~1024 workgroups of them;
+// below that one word per thread (more workgroups on small matrices: a 2048 x 1536
+// dequant took 3.6 us at U = 1 against 4.0 at U = 4).
+constexpr int64_t kWordsPerThreadMin = 1ll << 20;
+
 hipError_t w4l_unpack(const int32_t* pk, int8_t* q, int64_t nwords, hipStream_t st) {
-  const int block = 256;
-  const int64_t work = (nwords >> 2) > 0 ? (nwords >> 2) : 1;
-  hipLaunchKernelGGL(w4k::unpack_kernel, dim3(grid_for(work, block)), dim3(block), 0, st,
-                     reinterpret_cast<const uint32_t*>(pk), q, nwords);
+  const uint32_t* p = reinterpret_cast<const uint32_t*>(pk);
+  if (nwords >= kWordsPerThreadMin)
+    hipLaunchKernelGGL(w4k::unpack_kernel<4>, dim3((unsigned)((nwords + 1023) / 1024)), dim3(256), 0, st, p, q,
+                       nwords);
+  else
+    hipLaunchKernelGGL(w4k::unpack_kernel<1>, dim3((unsigned)((nwords + 255) / 256)), dim3(256), 0, st, p, q,
+                       nwords);
   return hipGetLastError();
 }
 
 hipError_t w4l_dequant(const int32_t* pk, const uint16_t* sc, uint16_t* w, int64_t N, int64_t K,
                        int32_t group, hipStream_t st) {
-  const int block = 256;
-  const int64_t nchunks = N * (K / 32);
-  hipLaunchKernelGGL(w4k::dequant_kernel, dim3(grid_for(nchunks, block)), dim3(block), 0, st,
-                     reinterpret_cast<const uint32_t*>(pk), sc, w, nchunks, K / 32, K / group,
-                     group / 32);
+  const int64_t nwords = N * (K / 8);
+  const int64_t wpg = group / 8;
+  const int shift = (wpg & (wpg - 1)) == 0 ? __builtin_ctzll((unsigned long long)wpg) : -1;
+  const uint32_t* p = reinterpret_cast<const uint32_t*>(pk);
+  if (nwords >= kWordsPerThreadMin)
+    hipLaunchKernelGGL(w4k::dequant_kernel<4>, dim3((unsigned)((nwords + 1023) / 1024)), dim3(256), 0, st, p, sc,
+                       w, nwords, wpg, shift);
+  else
+    hipLaunchKernelGGL(w4k::dequant_kernel<1>, dim3((unsigned)((nwords + 255) / 256)), dim3(256), 0, st, p, sc,
+                       w, nwords, wpg, shift);
   return hipGetLastError();
 }
 

@@ -139,20 +139,34 @@ def _dev_check(*ts) -> None:
             raise W4A16Error(EINVAL_SHAPE, "tensor must be contiguous (dense row-major)")
 
 
-def unpackW4(pk):
-    """int32 [N, K/8] -> int8 q [N, K] (w4.zig:33-45)."""
+def _out_check(out, shape, dtype, device, name):
+    """A caller-supplied output: the exact shape and dtype, dense, on pk's GPU."""
+    if tuple(out.shape) != tuple(shape) or out.dtype != dtype:
+        raise W4A16Error(EINVAL_SHAPE, f"{name} must be {dtype} {tuple(shape)}, got {out.dtype} {tuple(out.shape)}")
+    _dev_check(out)
+    if out.device != device:
+        raise W4A16Error(EINVAL_PTR, f"{name} is on {out.device}, pk on {device}")
+
+
+def unpackW4(pk, out=None):
+    """int32 [N, K/8] -> int8 q [N, K] (w4.zig:33-45).  out: optional int8 [N, K]."""
     torch = _torch()
     _dev_check(pk)
     if pk.dtype != torch.int32 or pk.dim() != 2:
         raise W4A16Error(EINVAL_ARG, "pk must be a 2-D int32 tensor")
     N, W = pk.shape
-    q = torch.empty((N, 8 * W), dtype=torch.int8, device=pk.device)
+    if out is None:
+        q = torch.empty((N, 8 * W), dtype=torch.int8, device=pk.device)
+    else:
+        _out_check(out, (N, 8 * W), torch.int8, pk.device, "out")
+        q = out
     check(lib().w4a16_unpack(pk.data_ptr(), q.data_ptr(), N, 8 * W, _stream_ptr(pk)))
     return q
 
 
-def dequantW4(pk, sc, group: int = GROUP):
-    """int32 pk [N, K/8] + bf16 sc [N, K/group] -> bf16 w [N, K] (w4.zig:47-54)."""
+def dequantW4(pk, sc, group: int = GROUP, out=None):
+    """int32 pk [N, K/8] + bf16 sc [N, K/group] -> bf16 w [N, K] (w4.zig:47-54).
+    out: optional bf16 [N, K]."""
     torch = _torch()
     _dev_check(pk, sc)
     if pk.dtype != torch.int32 or sc.dtype != torch.bfloat16 or pk.dim() != 2 or sc.dim() != 2:
@@ -161,7 +175,11 @@ def dequantW4(pk, sc, group: int = GROUP):
     K = 8 * W
     if sc.shape[0] != N or sc.shape[1] * group != K:
         raise W4A16Error(EINVAL_SHAPE, f"sc shape {tuple(sc.shape)} does not match pk {tuple(pk.shape)} / group {group}")
-    w = torch.empty((N, K), dtype=torch.bfloat16, device=pk.device)
+    if out is None:
+        w = torch.empty((N, K), dtype=torch.bfloat16, device=pk.device)
+    else:
+        _out_check(out, (N, K), torch.bfloat16, pk.device, "out")
+        w = out
     check(lib().w4a16_dequant(pk.data_ptr(), sc.data_ptr(), w.data_ptr(), N, K, group, _stream_ptr(pk)))
     return w
 

@@ -162,6 +162,31 @@ def test_w2_u1b_dequant_shape_families(name):
     assert np.array_equal(w4a16.unpackW4(dev(pk)).cpu().numpy(), o.unpack(pk))
 
 
+@pytest.mark.parametrize("N,K,group", [
+    (3, 24 * 4, 32), (5, 96, 96), (7, 256, 128), (333, 96, 32),     # word counts not a multiple of 256
+    (1024, 4096, 64), (2048, 3072, 96), (2048, 2048, 32),          # one word per thread
+    (4096, 8192, 64), (4096, 8448, 96), (4099, 8192, 32)])         # four words per thread (>= 4 Mi words)
+def test_dequant_unpack_launch_forms_and_groups(N, K, group):
+    """Both launch forms of the flat dequant/unpack (one or four words per thread),
+    the scale index as a shift (group / 8 a power of two) and as a division, and word
+    counts that leave partial workgroups: bit-exact against the oracle."""
+    say(f"dequant/unpack N={N} K={K} group={group}")
+    _, pk, sc = o.synth_weights(N, K, 4100 + N % 89, group=group)
+    ref = o.dequant(pk, sc, group)
+    got = host_u16(w4a16.dequantW4(dev(pk), dev_u16(sc), group=group))
+    assert np.array_equal(got, ref)
+    assert np.array_equal(w4a16.unpackW4(dev(pk)).cpu().numpy(), o.unpack(pk))
+    # caller-supplied outputs (filled with a pattern first): written in place
+    wbuf = torch.full((N, K), -1.0, dtype=torch.bfloat16, device="cuda")
+    assert w4a16.dequantW4(dev(pk), dev_u16(sc), group=group, out=wbuf) is wbuf
+    assert np.array_equal(host_u16(wbuf), ref)
+    qbuf = torch.full((N, K), 99, dtype=torch.int8, device="cuda")
+    assert w4a16.unpackW4(dev(pk), out=qbuf) is qbuf
+    assert np.array_equal(qbuf.cpu().numpy(), o.unpack(pk))
+    with pytest.raises(w4a16.W4A16Error):
+        w4a16.unpackW4(dev(pk), out=qbuf[:, :8])
+
+
 # ------------------------------------------------------------------ linear: exactness probes
 
 def test_linear_one_hot_reproduces_dequant_exactly():
