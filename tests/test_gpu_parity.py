@@ -165,7 +165,7 @@ def test_w2_u1b_dequant_shape_families(name):
 @pytest.mark.parametrize("N,K,group", [
     (3, 24 * 4, 32), (5, 96, 96), (7, 256, 128), (333, 96, 32),     # word counts not a multiple of 256
     (1024, 4096, 64), (2048, 3072, 96), (2048, 2048, 32),          # one word per thread
-    (4096, 8192, 64), (4096, 8448, 96), (4099, 8192, 32)])         # four words per thread (>= 4 Mi words)
+    (4096, 8192, 64), (4096, 8448, 96), (4099, 8192, 32)])         # four words per thread (>= 1 Mi words)
 def test_dequant_unpack_launch_forms_and_groups(N, K, group):
     """Both launch forms of the flat dequant/unpack (one or four words per thread),
     the scale index as a shift (group / 8 a power of two) and as a division, and word
@@ -760,6 +760,7 @@ def test_linear_m4_beyond_both_gemv_plans():
 
 @pytest.mark.parametrize("M,Ns,K,x_f32,out", [
     (1, (4096, 2048, 2048), 3840, False, "bf16"),   # 12B q, k, v at decode: one launch
+    (1, (8192, 512), 3840, False, "f32"),           # 12B full-attention q, k at decode: one launch
     (3, (17, 0, 33, 5), 512, False, "f32"),        # ragged N, an empty member
     (2, (64, 48), 1536, True, "f32"),               # f32 x
     (20, (40, 24, 16), 256, False, "bf16"),         # above M = 16: one launch per weight
