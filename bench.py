@@ -580,6 +580,15 @@ def main() -> int:
             table.append(r)
             log(f"{name:12s} M={M:5d} K={K:6d} F={F:6d}  fused {r['fused_us']:9.2f} us  unfused {r['unfused_us']:9.2f} us"
                 f"  {r['GBps']:8.1f} GB/s  {r['TFLOPs']:8.2f} TFLOP/s")
+        # w4a16_dequant / w4a16_unpack (W2/U1b shapes' largest matrices: 12B gate/up, down)
+        for name, N, K in [("deq_12B_gate_up", 30720, 3840), ("deq_12B_down", 3840, 15360)]:
+            r = time_dequant(torch, w4a16, N, K)
+            r["name"] = name
+            table.append(r)
+            log(f"{name:15s} N={N:6d} K={K:6d}  dequant {r['dequant']['avg_call_us']:8.2f} us"
+                f" ({r['dequant']['GBps']:7.1f} GB/s, {r['dequant']['hbm_frac'] * 100:4.1f} %)"
+                f"  unpack {r['unpack']['avg_call_us']:8.2f} us ({r['unpack']['GBps']:7.1f} GB/s,"
+                f" {r['unpack']['hbm_frac'] * 100:4.1f} %)")
         os.makedirs(os.path.join(ROOT, "gpurun_out"), exist_ok=True)
         with open(os.path.join(ROOT, "gpurun_out", "bench_all.json"), "w") as f:
             json.dump(table, f, indent=1)
