@@ -496,6 +496,51 @@ def test_linear_ragged(M, N, K, group):
     assert np.array_equal(host_u16(w4a16.dequantW4(dev(pk), dev_u16(sc), group)), w)
 
 
+def _random_linear_cases(n=64, seed=20261202):
+    """Seeded shapes over every route: M in the decode (1-4), 16-row (5-16), skinny
+    (17-64), mid (65-300) and prefill (512-1100) ranges, N ragged up to 6000, K a
+    multiple of the group up to 4096, groups 32 / 64 / 128, bf16 or f32 x, bf16 or f32 y,
+    with the optional split-K workspace or without it (one pass)."""
+    rng = np.random.Generator(np.random.PCG64(seed))
+    ranges = [(1, 4), (5, 16), (17, 64), (65, 300), (512, 1100)]
+    cases = []
+    for i in range(n):
+        lo, hi = ranges[i % len(ranges)]
+        M = int(rng.integers(lo, hi + 1))
+        group = int(rng.choice([32, 32, 64, 128]))
+        K = group * int(rng.integers(1, 4096 // group + 1))
+        N = int(rng.integers(1, 6001))
+        while M * N * K > 2_500_000_000:
+            N = max(1, N // 2)
+        x_f32 = bool(rng.random() < 0.25)
+        out = "f32" if (x_f32 or rng.random() < 0.5) else "bf16"
+        one_pass = (not x_f32) and bool(rng.random() < 0.5)
+        cases.append((i, M, N, K, group, x_f32, out, one_pass))
+    return cases
+
+
+@pytest.mark.parametrize("i,M,N,K,group,x_f32,out,one_pass", _random_linear_cases())
+def test_linear_random_shapes(i, M, N, K, group, x_f32, out, one_pass):
+    """Seeded random shapes through w4a16_linear against the oracle at the stated
+    tolerances (every output element)."""
+    say(f"random case {i}: M={M} N={N} K={K} group={group} x_f32={x_f32} out={out} one_pass={one_pass}")
+    _, pk, sc = o.synth_weights(N, K, 7000 + i, group)
+    xb = o.synth_x(M, K, 8000 + i)
+    x_np = (o.bf16_to_f32(xb) * np.float32(1.0 + 2.0 ** -10)).astype(np.float32) if x_f32 else xb
+    x = dev(x_np) if x_f32 else dev_u16(x_np)
+    ws = torch.empty(0, dtype=torch.uint8, device="cuda") if one_pass else None
+    odt = torch.float32 if out == "f32" else torch.bfloat16
+    y = w4a16.linear(x, dev(pk), dev_u16(sc), group=group, out_dtype=odt, workspace=ws)
+    torch.cuda.synchronize()
+    w = o.dequant(pk, sc, group)
+    if out == "f32":
+        check_f32(y.cpu().numpy(), x_np, w, K, x_f32=x_f32)
+    else:
+        ref32 = o.matmul_f32(xb, w)
+        _, mag = o.matmul_f64(xb, w)
+        check_bf16(host_u16(y), ref32, mag, K)
+
+
 def test_empty_and_k_zero():
     say("empty shapes / K = 0")
     x = torch.zeros((0, 64), dtype=torch.bfloat16, device="cuda")
