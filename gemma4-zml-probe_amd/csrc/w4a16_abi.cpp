@@ -249,9 +249,7 @@ int w4a16_linear_group(const void* x, int32_t x_dtype, int32_t n, const int32_t*
   } else if (workspace != nullptr && !aligned16(workspace)) {
     return fail(W4A16_EINVAL_PTR, "%s: workspace is not 16-byte aligned", fn);
   }
-  int64_t ntot = 0;
-  for (int j = 0; j < n; ++j) ntot += 16 * ((N[j] + 15) / 16);
-  if (w4l_group_fused(M, ntot, K, nterms))
+  if (w4l_group_fused(M, n, N, K, nterms))
     return hip_status(w4l_gemv_group(planes, nterms, n, pk, sc, y, N, y_f32, M, K, group, st), fn);
   // one launch each; with bf16 x and enough workspace a member takes the split-K
   // route as w4a16_linear would (the members run in stream order, so they share

@@ -660,10 +660,11 @@ __global__ void __launch_bounds__(1024) gemv_kernel(GemvArgs a) {
 // PLAIN: one matrix, no gate/up pair (a.pk, a.sc, a.y, a.N only): the kernel then
 // reads none of the group or pair arguments, whose selection the compiler turns into
 // branches with late scalar loads that delay every wave's first weight load.
-// S = 2 needs PLAIN, NT = 1, MR = 4, XW and M = 1 (checked on the host).
+// S = 2 needs NT = 1, MR = 4, XW, M = 1 and no gate/up pair (checked on the host): a
+// single weight (PLAIN) or a weight group, whose tiles are then 8-row tiles too.
 template <int NT, int NST, int XPT, bool G32, int MR, bool XW, bool PLAIN = false, int S = 1>
 __global__ void __launch_bounds__(1024) gemv_fast_kernel(GemvArgs a) {
-  static_assert(S == 1 || (S == 2 && PLAIN && NT == 1 && MR == 4 && XW), "K segments: plain M = 1 form only");
+  static_assert(S == 1 || (S == 2 && NT == 1 && MR == 4 && XW), "K segments: the bf16 M = 1 form only");
   constexpr int R = 16 / S;  // W rows per tile
   extern __shared__ __attribute__((aligned(16))) uint16_t lds[];
   const int lane = threadIdx.x & 63;
@@ -1808,13 +1809,16 @@ static hipError_t allow_big_lds(Kern k, size_t lds) {
 template <int NT, int NST, int XPT, int MR, bool XW, int S = 1>
 static hipError_t gemv_fast_one(const w4k::GemvArgs& a, dim3 grid, dim3 block, size_t lds, bool g32,
                                 hipStream_t st) {
-  // the plain single-matrix form for bf16 x with per-wave staging and the 4-row epilogue
+  // the plain single-matrix form for bf16 x with per-wave staging and the 4-row epilogue;
+  // K segments (S = 2) in that form or for a weight group (no gate/up pair), at M = 1
   constexpr bool PL = NT == 1 && MR == 4 && XW;
+  constexpr int S2 = PL ? S : 1;
   const bool plain = PL && a.nmat <= 1 && a.pair_f == 0;
-  if (S != 1 && !(plain && a.M == 1)) return hipErrorInvalidValue;
-  auto k = plain ? (g32 ? w4k::gemv_fast_kernel<NT, NST, XPT, true, MR, XW, PL, (PL ? S : 1)>
-                        : w4k::gemv_fast_kernel<NT, NST, XPT, false, MR, XW, PL, (PL ? S : 1)>)
-                 : (g32 ? w4k::gemv_fast_kernel<NT, NST, XPT, true, MR, XW> : w4k::gemv_fast_kernel<NT, NST, XPT, false, MR, XW>);
+  if (S != 1 && !(PL && a.pair_f == 0 && a.M == 1)) return hipErrorInvalidValue;
+  auto k = plain ? (g32 ? w4k::gemv_fast_kernel<NT, NST, XPT, true, MR, XW, PL, S2>
+                        : w4k::gemv_fast_kernel<NT, NST, XPT, false, MR, XW, PL, S2>)
+                 : (g32 ? w4k::gemv_fast_kernel<NT, NST, XPT, true, MR, XW, false, S2>
+                        : w4k::gemv_fast_kernel<NT, NST, XPT, false, MR, XW, false, S2>);
   hipError_t e = allow_big_lds(k, lds);
   if (e != hipSuccess) return e;
   hipLaunchKernelGGL(k, grid, block, lds, st, a);
@@ -1903,18 +1907,21 @@ static hipError_t gemv_fast_launch(const w4k::GemvArgs& a0, int nterms, int mr, 
   return hipErrorInvalidValue;
 }
 
+// Epilogue rows (4 or 16) and plan of the straight-line GEMV for N rows: the 4-row form
+// where its plan holds, else the 16-row form (M <= 16, bf16 x); 0 when neither holds.
+// K segments (8-row tiles) except for a gate/up pair.
+static int gemv_fast_plan(int64_t M, int64_t N, int64_t K, int nterms, bool pair, GemvPlan* p) {
+  if (w4l_gemv_ok(M, K, nterms) && gemv_plan(M, N, K, nterms, 4, p, !pair)) return 4;
+  if (gemv_plan(M, N, K, nterms, 16, p)) return 16;
+  return 0;
+}
+
 hipError_t w4l_gemv(const uint16_t* x_planes, int nterms, const int32_t* pk, const uint16_t* sc,
                     void* y, int y_f32, int64_t M, int64_t N, int64_t K, int32_t group,
                     hipStream_t st, const W4Pair* pair) {
   if (pair) N = 16 * ((pair->F + 7) / 8);
-  // the 4-row form where its plan holds, else the 16-row form (M <= 16, bf16 x)
-  // K segments (8-row tiles) only for the plain single-matrix form
   GemvPlan p;
-  int mr = 4;
-  if (!(w4l_gemv_ok(M, K, nterms) && gemv_plan(M, N, K, nterms, 4, &p, pair == nullptr))) {
-    mr = 16;
-    if (!gemv_plan(M, N, K, nterms, 16, &p)) mr = 0;
-  }
+  const int mr = gemv_fast_plan(M, N, K, nterms, pair != nullptr, &p);
   w4k::GemvArgs a{};
   a.x = x_planes;
   a.pk = reinterpret_cast<const uint32_t*>(pk);
@@ -2383,24 +2390,45 @@ hipError_t w4l_gelu_mul(const float* g, const float* u, void* h, int h_f32, int 
   return hipGetLastError();
 }
 
-bool w4l_group_fused(int64_t M, int64_t Ntot, int64_t K, int nterms) {
-  if (M <= 4 && w4l_gemv_fast_ok(M, Ntot, K, nterms)) return true;
-  return w4l_gemv16_ok(M, Ntot, K, nterms);
+// The plan every member of a weight group gets from w4l_linear on its own, when they all
+// run the straight-line GEMV with the same plan: one launch then gives each y_j exactly
+// the single call's result (same tiles per row, same runs of steps, same summation
+// order).  Returns the epilogue rows (0: no common plan, so one launch per member).
+static int group_common_plan(int64_t M, int n, const int64_t* N, int64_t K, int nterms, GemvPlan* p) {
+  int mr = 0;
+  for (int j = 0; j < n; ++j) {
+    if (!N[j]) continue;
+    // w4l_linear's first two routes are the ones that reach this GEMV
+    if (!w4l_gemv_fast_ok(M, N[j], K, nterms) && !w4l_gemv16_ok(M, N[j], K, nterms)) return 0;
+    GemvPlan q;
+    const int m = gemv_fast_plan(M, N[j], K, nterms, false, &q);
+    if (!m) return 0;
+    if (!mr) {
+      mr = m;
+      *p = q;
+    } else if (m != mr || q.s != p->s || q.waves != p->waves || q.nst != p->nst || q.xpt != p->xpt || q.xw != p->xw) {
+      return 0;
+    }
+  }
+  return mr;
+}
+
+bool w4l_group_fused(int64_t M, int n, const int64_t* N, int64_t K, int nterms) {
+  int64_t ntot = 0;
+  for (int j = 0; j < n; ++j) ntot += 16 * ((N[j] + 15) / 16);
+  const bool fits = (M <= 4 && w4l_gemv_fast_ok(M, ntot, K, nterms)) || w4l_gemv16_ok(M, ntot, K, nterms);
+  GemvPlan p;
+  return fits && group_common_plan(M, n, N, K, nterms, &p) != 0;
 }
 
 hipError_t w4l_gemv_group(const uint16_t* x_planes, int nterms, int n, const int32_t* const* pk,
                           const uint16_t* const* sc, void* const* y, const int64_t* N, int y_f32, int64_t M, int64_t K,
                           int32_t group, hipStream_t st) {
   if (n < 1 || n > 4) return hipErrorInvalidValue;
-  int64_t ntot = 0;
-  for (int j = 0; j < n; ++j) ntot += 16 * ((N[j] + 15) / 16);
-  // the 4-row form where its plan holds, else the 16-row form (M <= 16)
   GemvPlan p;
-  int mr = 4;
-  if (!(w4l_gemv_ok(M, K, nterms) && gemv_plan(M, ntot, K, nterms, 4, &p))) {
-    mr = 16;
-    if (!gemv_plan(M, ntot, K, nterms, 16, &p)) return hipErrorInvalidValue;
-  }
+  const int mr = group_common_plan(M, n, N, K, nterms, &p);
+  if (!mr) return hipErrorInvalidValue;
+  const int R = 16 / p.s;  // W rows per tile
   w4k::GemvArgs a{};
   a.x = x_planes;
   a.M = (int)M;
@@ -2417,7 +2445,7 @@ hipError_t w4l_gemv_group(const uint16_t* x_planes, int nterms, int n, const int
     a.gy[j] = y[j];
     a.gN[j] = (int)N[j];
     a.tile0[j] = (int)tiles;
-    tiles += (N[j] + 15) / 16;
+    tiles += (N[j] + R - 1) / R;
   }
   // a matrix with N = 0 owns no tiles; the single-matrix fields stay those of matrix 0
   a.pk = a.gpk[0];

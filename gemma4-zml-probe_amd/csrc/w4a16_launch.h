@@ -57,9 +57,10 @@ hipError_t w4l_prefill(const uint16_t* x, const int32_t* pk, const uint16_t* sc,
                        const W4Pair* pair = nullptr);
 
 // Weight group: n <= 4 linears [N_j, K] that read the same x (q, k, v), one
-// launch of the straight-line GEMV when w4l_group_fused; otherwise the caller
-// runs w4l_linear per weight.
-bool w4l_group_fused(int64_t M, int64_t Ntot, int64_t K, int nterms);
+// launch of the straight-line GEMV when w4l_group_fused (every member would run that
+// GEMV with the same plan on its own, so each y_j equals w4l_linear's bit for bit);
+// otherwise the caller runs w4l_linear per weight.
+bool w4l_group_fused(int64_t M, int n, const int64_t* N, int64_t K, int nterms);
 hipError_t w4l_gemv_group(const uint16_t* x_planes, int nterms, int n, const int32_t* const* pk,
                           const uint16_t* const* sc, void* const* y, const int64_t* N, int y_f32, int64_t M, int64_t K,
                           int32_t group, hipStream_t st);

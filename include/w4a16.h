@@ -168,8 +168,10 @@ int w4a16_linear_noalloc(const void *x, int32_t x_dtype,
  * Several linears that read the same activations, y_j[M, N_j] = x[M, K] .
  * dequantW4(pk_j, sc_j)^T for j < n (1 <= n <= 4): q, k and v of a layer, which all
  * take the normed hidden h0 (zml_runner/engine.zig:552,571,583).  Each y_j is
- * exactly what w4a16_linear gives for that weight; at decode (M <= 4) the n
- * linears run as one launch, otherwise one launch each.  pk, sc, y and N are
+ * exactly what w4a16_linear gives for that weight; at decode (M <= 16) the n
+ * linears run as one launch when every one of them would take the same decode
+ * GEMV plan on its own (the 12B and E2B q/k/v shapes do), otherwise one launch
+ * each.  pk, sc, y and N are
  * host arrays of n entries; every weight has K columns and the same group.
  * Workspace as w4a16_linear: f32 x needs w4a16_workspace_size(M, 0, K, x_dtype);
  * with bf16 x, optional, each member that runs as its own launch takes the

@@ -806,6 +806,7 @@ def test_linear_m4_beyond_both_gemv_plans():
 @pytest.mark.parametrize("M,Ns,K,x_f32,out", [
     (1, (4096, 2048, 2048), 3840, False, "bf16"),   # 12B q, k, v at decode: one launch
     (1, (8192, 512), 3840, False, "f32"),           # 12B full-attention q, k at decode: one launch
+    (1, (2048, 256, 256), 1536, False, "f32"),      # E2B q, k, v at decode (K % 512 == 0: the single linears split K in two)
     (3, (17, 0, 33, 5), 512, False, "f32"),        # ragged N, an empty member
     (2, (64, 48), 1536, True, "f32"),               # f32 x
     (20, (40, 24, 16), 256, False, "bf16"),         # above M = 16: one launch per weight
