@@ -836,3 +836,39 @@ def test_linear_group_equals_single_linears(M, Ns, K, x_f32, out):
     if Ns[0] and out == "f32":
         w = o.dequant(*ws[0])
         check_f32(ys[0].cpu().numpy(), x_np, w, K, x_f32=x_f32)
+
+
+def _random_group_cases(n=24, seed=20261204):
+    """Seeded weight groups: 1-4 members of ragged N (an empty one now and then), M 1-20,
+    K a multiple of 32 up to 4096 (K % 512 == 0 half the time: the K-segment plans), bf16
+    or f32 x, bf16 or f32 y."""
+    rng = np.random.Generator(np.random.PCG64(seed))
+    cases = []
+    for i in range(n):
+        M = int(rng.choice([1, 1, 1, 2, 3, 4, 5, 8, 13, 16, 20]))
+        K = 512 * int(rng.integers(1, 9)) if rng.random() < 0.5 else 32 * int(rng.integers(1, 129))
+        Ns = tuple(int(v) if rng.random() > 0.1 else 0 for v in rng.integers(1, 9000, size=int(rng.integers(1, 5))))
+        x_f32 = bool(rng.random() < 0.2)
+        out = "f32" if rng.random() < 0.5 else "bf16"
+        cases.append((i, M, Ns, K, x_f32, out))
+    return cases
+
+
+@pytest.mark.parametrize("i,M,Ns,K,x_f32,out", _random_group_cases())
+def test_linear_group_random_equals_single_linears(i, M, Ns, K, x_f32, out):
+    """Seeded random groups: every output of w4a16_linear_group equals w4a16_linear of
+    that weight bit for bit (fused or not)."""
+    say(f"random linear_group {i}: M={M} Ns={Ns} K={K} x_f32={x_f32} out={out}")
+    ws = [o.synth_weights(n, K, 300 + 7 * i + j)[1:] for j, n in enumerate(Ns)]
+    x_np = o.synth_x(M, K, 400 + i)
+    if x_f32:
+        x_np = (o.bf16_to_f32(x_np) * np.float32(1.0 + 2.0 ** -10)).astype(np.float32)
+    x = dev(x_np) if x_f32 else dev_u16(x_np)
+    lins = [w4a16.W4Lin(dev(pk), dev_u16(sc)) for pk, sc in ws]
+    odt = torch.float32 if out == "f32" else torch.bfloat16
+    ys = w4a16.linear_group(x, lins, out_dtype=odt)
+    singles = [w4a16.linear(x, lin.pk, lin.sc, out_dtype=odt) for lin in lins]
+    torch.cuda.synchronize()
+    for y, y1 in zip(ys, singles):
+        assert torch.equal(y.view(torch.int32 if out == "f32" else torch.int16),
+                           y1.view(torch.int32 if out == "f32" else torch.int16))
