@@ -37,12 +37,17 @@ struct HeadArgs {
   float* logits;      // [M][V] f32
   int M, V, K;
   float cap;          // softcap; 0 = none
+  // runs of 32-column steps: the first wrem waves take wbase + 1 steps, the others
+  // wbase (wrem = 0 when the waves split K evenly)
+  int wbase, wrem;
 };
 
-// NT: bf16 planes of x (1, or 3 for f32 x).  NST: 32-column steps per wave.
-// XPT: x vectors (16 B) per thread.  Waves = blockDim.x / 64; wave w covers
-// steps [w * NST, (w + 1) * NST), and waves * NST * 32 == K.  MR: rows of x
-// the epilogue covers, 4 or 16 (the MFMA's A operand holds 16 rows either way).
+// NT: bf16 planes of x (1, or 3 for f32 x).  NST: the longest run of 32-column steps
+// of a wave.  XPT: x vectors (16 B) per thread.  Waves = blockDim.x / 64; wave w covers
+// steps [s0, s0 + cnt) with cnt = wbase + (w < wrem) and s0 = w * wbase + min(w, wrem),
+// so the runs tile K / 32 steps in order; a run one step short loads its last step
+// twice and skips the duplicate's MFMAs (a wave-uniform branch).  MR: rows of x the
+// epilogue covers, 4 or 16 (the MFMA's A operand holds 16 rows either way).
 template <int NT, int NST, int XPT, int MR = 4>
 __global__ void __launch_bounds__(1024) head_logits_kernel(HeadArgs a) {
   extern __shared__ __attribute__((aligned(16))) uint16_t lds[];
@@ -64,11 +69,13 @@ __global__ void __launch_bounds__(1024) head_logits_kernel(HeadArgs a) {
     const int t = NT == 1 ? 0 : xi[i] / pv;
     xv[i] = xsrc[t * (a.xplane >> 3) + (xi[i] - t * pv)];
   }
+  const int cnt = a.wbase + (wave < a.wrem ? 1 : 0);
+  const int s0 = wave * a.wbase + min(wave, a.wrem);
   const int n = min((int)blockIdx.x * 16 + r, a.V - 1);
-  const uint16_t* erow = a.e + (int64_t)n * a.K + wave * NST * 32 + 8 * c;
+  const uint16_t* erow = a.e + (int64_t)n * a.K + s0 * 32 + 8 * c;
   uint4 wv[NST];
 #pragma unroll
-  for (int i = 0; i < NST; ++i) wv[i] = *reinterpret_cast<const uint4*>(erow + 32 * i);
+  for (int i = 0; i < NST; ++i) wv[i] = *reinterpret_cast<const uint4*>(erow + 32 * (i < NST - 1 ? i : min(i, cnt - 1)));
 
   uint4* xdst = reinterpret_cast<uint4*>(lds);
 #pragma unroll
@@ -77,13 +84,15 @@ __global__ void __launch_bounds__(1024) head_logits_kernel(HeadArgs a) {
 
   // A: lane (r, c) holds x[m = r][8c .. 8c+7] of the step (rows past M repeat M-1)
   const int plane = a.M * a.K;
-  const uint16_t* xrow = lds + min(r, a.M - 1) * a.K + wave * NST * 32 + 8 * c;
+  const uint16_t* xrow = lds + min(r, a.M - 1) * a.K + s0 * 32 + 8 * c;
   floatx4 acc[1] = {floatx4{0.f, 0.f, 0.f, 0.f}};
 #pragma unroll
   for (int i = 0; i < NST; ++i) {
-    const bf16x8 b = __builtin_bit_cast(bf16x8, wv[i]);
+    if (i < NST - 1 || i < cnt) {
+      const bf16x8 b = __builtin_bit_cast(bf16x8, wv[i]);
 #pragma unroll
-    for (int t = 0; t < NT; ++t) mfma_acc(acc[0], *reinterpret_cast<const bf16x8*>(xrow + t * plane + 32 * i), b);
+      for (int t = 0; t < NT; ++t) mfma_acc(acc[0], *reinterpret_cast<const bf16x8*>(xrow + t * plane + 32 * i), b);
+    }
   }
   mfma_drain<1>(acc);
 
@@ -138,13 +147,16 @@ __global__ void __launch_bounds__(1024) head_loop_kernel(HeadArgs a, int per) {
     const int t = NT == 1 ? 0 : xi[i] / pv;
     xv[i] = xsrc[t * (a.xplane >> 3) + (xi[i] - t * pv)];
   }
+  const int cnt = a.wbase + (wave < a.wrem ? 1 : 0);
+  const int s0 = wave * a.wbase + min(wave, a.wrem);
   uint4 wv[2][NST];
   auto wload = [&](auto b_c, int tile) __attribute__((always_inline)) {
     constexpr int b = decltype(b_c)::value;
     const int n = min(min(tile, tend - 1) * 16 + r, a.V - 1);
-    const uint16_t* erow = a.e + (int64_t)n * a.K + wave * NST * 32 + 8 * c;
+    const uint16_t* erow = a.e + (int64_t)n * a.K + s0 * 32 + 8 * c;
 #pragma unroll
-    for (int i = 0; i < NST; ++i) wv[b][i] = *reinterpret_cast<const uint4*>(erow + 32 * i);
+    for (int i = 0; i < NST; ++i)
+      wv[b][i] = *reinterpret_cast<const uint4*>(erow + 32 * (i < NST - 1 ? i : min(i, cnt - 1)));
   };
   wload(std::integral_constant<int, 0>{}, t0);
   uint4* xdst = reinterpret_cast<uint4*>(lds);
@@ -153,16 +165,18 @@ __global__ void __launch_bounds__(1024) head_loop_kernel(HeadArgs a, int per) {
   __syncthreads();
 
   const int plane = a.M * a.K;
-  const uint16_t* xrow = lds + min(r, a.M - 1) * a.K + wave * NST * 32 + 8 * c;
+  const uint16_t* xrow = lds + min(r, a.M - 1) * a.K + s0 * 32 + 8 * c;
   float* red = reinterpret_cast<float*>(lds + NT * plane);  // [waves][MR][16]
   auto compute = [&](auto b_c, int tile) __attribute__((always_inline)) {
     constexpr int b = decltype(b_c)::value;
     floatx4 acc[1] = {floatx4{0.f, 0.f, 0.f, 0.f}};
 #pragma unroll
     for (int i = 0; i < NST; ++i) {
-      const bf16x8 w = __builtin_bit_cast(bf16x8, wv[b][i]);
+      if (i < NST - 1 || i < cnt) {
+        const bf16x8 w = __builtin_bit_cast(bf16x8, wv[b][i]);
 #pragma unroll
-      for (int t = 0; t < NT; ++t) mfma_acc(acc[0], *reinterpret_cast<const bf16x8*>(xrow + t * plane + 32 * i), w);
+        for (int t = 0; t < NT; ++t) mfma_acc(acc[0], *reinterpret_cast<const bf16x8*>(xrow + t * plane + 32 * i), w);
+      }
     }
     mfma_drain<1>(acc);
     if (MR == 16 || c == 0) {
@@ -289,8 +303,18 @@ __global__ void __launch_bounds__(TOPK_THREADS) topk_merge_kernel(const uint64_t
 
 // ---------------------------------------------------------------- launchers
 
+// Where no even split exists (a step count with no divisor pair within 16 x 16, e.g.
+// 37 steps at K = 1184): runs of at most nst = ceil(steps / 16) steps over
+// ceil(steps / nst) waves (<= 16), up to 256 steps (K <= 8192).
+static bool head_plan_runs(int64_t steps, int* nst, int* waves) {
+  if (steps < 1 || steps > 256) return false;
+  *nst = (int)((steps + 15) / 16);
+  *waves = (int)((steps + *nst - 1) / *nst);
+  return true;
+}
+
 // Steps per wave for K / 32 steps: the divisor <= 16 that gives the wave count
-// closest to 8 (at most 16 waves).
+// closest to 8 (at most 16 waves); else uneven runs.
 static bool head_plan(int64_t K, int* nst, int* waves) {
   if (K % 32 != 0) return false;
   const int64_t steps = K / 32;
@@ -299,7 +323,7 @@ static bool head_plan(int64_t K, int* nst, int* waves) {
     if (steps % d != 0 || steps / d > 16) continue;
     if (!best || llabs(steps / d - 8) < llabs(steps / best - 8)) best = d;
   }
-  if (!best) return false;
+  if (!best) return head_plan_runs(steps, nst, waves);
   *nst = best;
   *waves = (int)(steps / best);
   return true;
@@ -307,7 +331,7 @@ static bool head_plan(int64_t K, int* nst, int* waves) {
 
 // More rows per launch (5..16) use the MR = 16 epilogue and the plan with the
 // most waves (<= 16), so that each thread stages <= 8 x vectors; x then takes
-// up to 160 KB of LDS.
+// up to 160 KB of LDS.  Uneven runs where no even split exists.
 static bool head_plan16(int64_t K, int* nst, int* waves) {
   if (K % 32 != 0) return false;
   const int64_t steps = K / 32;
@@ -317,7 +341,7 @@ static bool head_plan16(int64_t K, int* nst, int* waves) {
       *waves = (int)(steps / d);
       return true;
     }
-  return false;
+  return head_plan_runs(steps, nst, waves);
 }
 static bool head_fits(int64_t K, int nterms, int mc, int waves, int mr) {
   const int64_t xbytes = (int64_t)nterms * mc * K * 2;
@@ -352,6 +376,9 @@ hipError_t w4l_head_logits(const uint16_t* x_planes, int64_t xplane, int nterms,
   a.V = (int)V;
   a.K = (int)K;
   a.cap = cap;
+  a.wbase = (int)(K / 32 / waves);
+  a.wrem = (int)(K / 32 % waves);
+  if ((K / 32 + waves - 1) / waves != nst) return hipErrorInvalidValue;
   const int64_t nvec = (int64_t)nterms * M * K / 8;
   const int64_t per = (nvec + 64 * waves - 1) / (64 * waves);
   int xpt = 1;

@@ -254,7 +254,7 @@ size_t w4a16_lm_head_workspace_size(int64_t M, int64_t V, int64_t K, int32_t x_d
  *                    descending; equal values in ascending index order; NaN counts as larger
  *                    than +inf.  NaN logits are written as the quiet NaN 0x7FC00000.
  *   x_dtype   W4A16_DTYPE_BF16 or W4A16_DTYPE_F32 (carried exactly, as in w4a16_linear).
- *   embed     bf16 [V, K], row-major; K % 32 == 0.
+ *   embed     bf16 [V, K], row-major; K % 32 == 0 and K <= 8192 (W4A16_EINVAL_SHAPE otherwise).
  *   logits    f32 [M, V] output (the step returns it alongside the top-k).
  *   topk      0..64 with topk <= V and ceil(V / 4096) * topk <= 4096; 0 skips the top-k
  *             (top_values / top_indices may then be NULL).

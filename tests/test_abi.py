@@ -338,6 +338,7 @@ def _lm(L, x=A, xd=0, e=A, lg=A, M=1, V=1000, K=256, cap=30.0, k=5, tv=A, ti=A, 
 def test_lm_head_validation(L):
     assert _lm(L, M=-1) == w4a16.EINVAL_SHAPE
     assert _lm(L, K=48) == w4a16.EINVAL_SHAPE              # K % 32
+    assert _lm(L, K=8224) == w4a16.EINVAL_SHAPE            # K > 8192: no launch plan (bf16 x: before any HIP call)
     assert _lm(L, xd=2) == w4a16.EINVAL_ARG
     assert _lm(L, cap=-1.0) == w4a16.EINVAL_ARG
     assert _lm(L, cap=float("nan")) == w4a16.EINVAL_ARG

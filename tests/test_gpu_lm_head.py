@@ -102,6 +102,37 @@ def test_lm_head_vs_oracle(M, V, K, x_f32, cap, k):
     check(x, e, lg, vals, idx, K, cap, k)
 
 
+def _random_head_cases(n=24, seed=20261205):
+    """Seeded heads: M 1-24, V ragged up to 40000, K a multiple of 32 up to 4096, bf16 or
+    f32 x, softcap 30 or none, top-k 0-64."""
+    rng = np.random.Generator(np.random.PCG64(seed))
+    cases = []
+    for i in range(n):
+        M = int(rng.integers(1, 25))
+        V = int(rng.integers(1, 40001))
+        K = 32 * int(rng.integers(1, 129))
+        while M * V * K > 1_500_000_000:
+            V = max(1, V // 2)
+        x_f32 = bool(rng.random() < 0.3)
+        cap = 30.0 if rng.random() < 0.7 else 0.0
+        k = int(rng.choice([0, 1, 2, 5, 8, 17, 64]))
+        cases.append((i, M, V, K, x_f32, cap, min(k, V)))
+    return cases
+
+
+@pytest.mark.parametrize("i,M,V,K,x_f32,cap,k", _random_head_cases())
+def test_lm_head_random_shapes(i, M, V, K, x_f32, cap, k):
+    """Seeded random heads against the oracle at the stated tolerance; top-k bit-equal
+    to the oracle's top-k of the GPU logits and to the float64 ranking on decisive rows."""
+    say(f"random lm_head {i}: M={M} V={V} K={K} x_f32={x_f32} cap={cap} k={k}")
+    e = synth_embed(V, K, 6000 + i)
+    x = o.synth_x(M, K, 6100 + i)
+    if x_f32:
+        x = (o.bf16_to_f32(x) * np.float32(1.0 + 2.0 ** -10)).astype(np.float32)
+    lg, vals, idx = run(x, dev_bf16(e), cap, k)
+    check(x, e, lg, vals, idx, K, cap, k)
+
+
 def test_lm_head_12b_vocab():
     """The 12B head: V = 262144, K = 3840 (a 2 GB bf16 embedding), M = 1, top-5."""
     V, K = 262144, 3840
