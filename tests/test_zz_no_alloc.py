@@ -87,3 +87,22 @@ def test_noalloc_rejects_f32_beyond_scratch():
                                 None)
     assert rc == w4a16.EWORKSPACE
     assert "scratch" in L.w4a16_last_error().decode()
+
+
+def test_noalloc_random_sequence():
+    """Sixteen seeded calls in a row with random shapes (M 1-64, ragged N, K up to 8192,
+    bf16 or f32 x within the scratch, bf16 or f32 y): each output equals w4a16_linear's
+    with an 8 MiB workspace bit for bit, whatever the previous call left in the scratch."""
+    rng = np.random.Generator(np.random.PCG64(20261206))
+    for i in range(16):
+        M = int(rng.integers(1, 65))
+        K = 32 * int(rng.integers(1, 257))
+        N = int(rng.integers(1, 6001))
+        x_f32 = bool(rng.random() < 0.3) and 6 * M * K <= SCRATCH
+        out_f32 = bool(rng.random() < 0.5)
+        say(f"random call {i}: M={M} N={N} K={K} x_f32={x_f32} out_f32={out_f32}")
+        x, pk, sc = _inputs(M, N, K, x_f32, 1000 + i)
+        ref, got = _call_both(x, pk, sc, M, N, K, out_f32)
+        a = ref.view(torch.int32 if out_f32 else torch.int16).cpu().numpy()
+        b = got.view(torch.int32 if out_f32 else torch.int16).cpu().numpy()
+        assert np.array_equal(a, b), (i, int(np.sum(a != b)))
