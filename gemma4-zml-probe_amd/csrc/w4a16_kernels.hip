@@ -20,6 +20,7 @@
 #include <stdint.h>
 #include <stdlib.h>
 
+#include <atomic>
 #include <type_traits>
 
 #include "w4a16_device.h"
@@ -453,6 +454,10 @@ struct GemvArgs {
   // gemv_fast_kernel: steps of GSTEP columns per wave within one K segment; the
   // first wrem waves of a workgroup take wbase + 1 steps, the others wbase
   int wbase, wrem;
+  // gemv_fast_kernel: tiles of the launch, and the grid size: workgroup b takes tiles b,
+  // b + gstride, ... (kept next to wbase and wrem, so that all of them arrive in the
+  // kernel's first batch of argument loads)
+  int ntiles, gstride, waves;  // (waves = blockDim.x / 64)
   // gate/up pair mode (gemv_fast_kernel only): pk/sc are gate, pk2/sc2 up,
   // pair_f = F real rows each (0 = plain linear), N = 16 * ceil(F / 8).
   const uint32_t* pk2;
@@ -630,7 +635,8 @@ __global__ void __launch_bounds__(1024) gemv_kernel(GemvArgs a) {
 // Same lane layout as gemv_kernel, for K a multiple of GSTEP * S.  A workgroup covers
 // one tile of R = 16 / S rows of W; its waves split each of the S K segments of the
 // tile's rows into runs of steps (wbase + 1 steps for the first wrem waves, wbase for
-// the others; NST = the longer run, a compile-time bound).
+// the others; NST = the longer run, a compile-time bound).  LOOP: a grid of at most
+// one round of workgroups walks the tiles (b, b + gstride, ...), see below.
 //
 // K segments (S = 2, M = 1 only): the MFMA's 16 B-operand columns are R rows x S
 // segments of K -- lane r holds row r % R in segment r / R -- and its A operand row r
@@ -662,7 +668,7 @@ __global__ void __launch_bounds__(1024) gemv_kernel(GemvArgs a) {
 // branches with late scalar loads that delay every wave's first weight load.
 // S = 2 needs NT = 1, MR = 4, XW, M = 1 and no gate/up pair (checked on the host): a
 // single weight (PLAIN) or a weight group, whose tiles are then 8-row tiles too.
-template <int NT, int NST, int XPT, bool G32, int MR, bool XW, bool PLAIN = false, int S = 1>
+template <int NT, int NST, int XPT, bool G32, int MR, bool XW, bool PLAIN = false, int S = 1, bool LOOP = false>
 __global__ void __launch_bounds__(1024) gemv_fast_kernel(GemvArgs a) {
   static_assert(S == 1 || (S == 2 && NT == 1 && MR == 4 && XW), "K segments: the bf16 M = 1 form only");
   // Wave priority: high until every load of the wave is issued (a wave that has just
@@ -674,23 +680,24 @@ __global__ void __launch_bounds__(1024) gemv_fast_kernel(GemvArgs a) {
   extern __shared__ __attribute__((aligned(16))) uint16_t lds[];
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-  const int nwaves = blockDim.x >> 6;
+  const int nwaves = a.waves;  // blockDim.x / 64, from the first batch of argument loads
   const int r = lane & 15;
   const int c = lane >> 4;
   const int seg = r / R, rr = r % R;  // B column r: row rr of the tile, K segment seg
   // this wave's run of steps in every segment: [s0, s0 + cnt), cnt = NST or NST - 1
   const int cnt = a.wbase + (wave < a.wrem ? 1 : 0);
   const int s0 = wave * a.wbase + min(wave, a.wrem);
-  // the block's matrix (a weight group's member, or the single weight) and its tile
-  const GroupSel gs = PLAIN ? GroupSel{a.pk, a.sc, a.y, a.N, 0} : group_select(a, (int)blockIdx.x);
-  const int pair_f = PLAIN ? 0 : a.pair_f;
-  const int N = gs.N;
-  const int bt = (int)blockIdx.x - gs.tile0;
   const int K = a.K;
   const int KS = (int)((unsigned)K / S);  // columns per segment
   const int plane = a.M * K;
+  // LOOP (the PLAIN form with group-32 scales): workgroup b takes tiles b, b + gstride,
+  // ... of a grid the host caps at one round; the next tile's loads go out before the
+  // current tile's epilogue and x is staged once.  Otherwise one tile per workgroup.
+  static_assert(!LOOP || (PLAIN && G32 && S == 1), "tile loop: the PLAIN group-32 form");
+  constexpr bool PERSIST = LOOP;
+  const int T = a.ntiles;  // (gridDim.x is a.gstride)
 
-  // 1. x loads, first (they need nothing but x's address)
+  // 1. x loads, first (they need nothing but x's address; x is the same for every tile)
   typedef __attribute__((address_space(1))) const u32x4 g_u4;
   typedef __attribute__((address_space(1))) const uint32_t g_u32;
   const u32x4* xsrc = reinterpret_cast<const u32x4*>(a.x);
@@ -712,49 +719,56 @@ __global__ void __launch_bounds__(1024) gemv_fast_kernel(GemvArgs a) {
   } else {
     const int nvec = (NT * plane) >> 3;
 #pragma unroll
-    for (int i = 0; i < XPT; ++i) xi[i] = min((int)threadIdx.x + i * (int)blockDim.x, nvec - 1);
+    for (int i = 0; i < XPT; ++i) xi[i] = min((int)threadIdx.x + i * 64 * nwaves, nvec - 1);
   }
   u32x4 xv[XPT];
 #pragma unroll
   for (int i = 0; i < XPT; ++i) xv[i] = xsrc[xi[i]];
   __builtin_amdgcn_sched_barrier(0);
 
-  // row pointers (pinned in VGPRs as global-memory pointers, so that the compiler
-  // forms no address between the loads below)
-  const int tile = min(bt, (N + R - 1) / R - 1);
-  const uint32_t* pkrow;
-  const uint16_t* scrow;
-  weight_row(gs.pk, gs.sc, a.pk2, a.sc2, pair_f, tile * R + rr, N, K, a.groups_per_row, pkrow, scrow);
-  // first 32-column chunk of this lane's run: segment start, run start, lane group
-  const int cb = seg * (KS >> 5) + s0 * 8 + c * 2;
-  g_u4* wb = (g_u4*)(reinterpret_cast<const u32x4*>(pkrow) + cb);
-  g_u32* sb = (g_u32*)(reinterpret_cast<const uint32_t*>(scrow) + (cb >> 1));
-  asm volatile("" : "+v"(wb), "+v"(sb));
-  __builtin_amdgcn_sched_barrier(0);
-
-  // 2. scales, then 3. weights, of this wave's NST steps (the last one clamped into
-  // the run: a short run loads its last step twice)
+  // 2. scales, then 3. weights, of this wave's NST steps of tile t (the last one clamped
+  // into the run: a short run loads its last step twice).  The tile's matrix (a weight
+  // group's member, or the single weight) and row pointers are formed first and pinned
+  // in VGPRs as global-memory pointers, so that the compiler forms no address between
+  // the loads.
+  const int pair_f = PLAIN ? 0 : a.pair_f;
+  const int cb = seg * (KS >> 5) + s0 * 8 + c * 2;  // first 32-column chunk of the lane's run
   auto step_of = [&](int i) { return i < NST - 1 ? i : min(i, cnt - 1); };
-  uint32_t sv[NST];  // two bf16 scales (low half: the step's first vector)
-  if (G32) {
+  GroupSel gs;
+  int bt;                // tile index within its matrix
+  uint32_t sv[NST];      // two bf16 scales (low half: the step's first vector)
+  u32x4 wv[NST][VPL];
+  auto issue = [&](int t) __attribute__((always_inline)) {
+    gs = PLAIN ? GroupSel{a.pk, a.sc, a.y, a.N, 0} : group_select(a, t);
+    bt = t - gs.tile0;
+    const int tile = min(bt, (gs.N + R - 1) / R - 1);
+    const uint32_t* pkrow;
+    const uint16_t* scrow;
+    weight_row(gs.pk, gs.sc, a.pk2, a.sc2, pair_f, tile * R + rr, gs.N, K, a.groups_per_row, pkrow, scrow);
+    g_u4* wb = (g_u4*)(reinterpret_cast<const u32x4*>(pkrow) + cb);
+    g_u32* sb = (g_u32*)(reinterpret_cast<const uint32_t*>(scrow) + (cb >> 1));
+    asm volatile("" : "+v"(wb), "+v"(sb));
+    __builtin_amdgcn_sched_barrier(0);
+    if (G32) {
 #pragma unroll
-    for (int i = 0; i < NST; ++i) sv[i] = sb[4 * step_of(i)];
-  } else {
+      for (int i = 0; i < NST; ++i) sv[i] = sb[4 * step_of(i)];
+    } else {
+#pragma unroll
+      for (int i = 0; i < NST; ++i) {
+        const int g0 = cb + 8 * step_of(i);
+        sv[i] = (uint32_t)scrow[g0 / a.group_chunks] | ((uint32_t)scrow[(g0 + 1) / a.group_chunks] << 16);
+      }
+    }
+    __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
     for (int i = 0; i < NST; ++i) {
-      const int g0 = cb + 8 * step_of(i);
-      sv[i] = (uint32_t)scrow[g0 / a.group_chunks] | ((uint32_t)scrow[(g0 + 1) / a.group_chunks] << 16);
+      wv[i][0] = wb[8 * step_of(i)];
+      wv[i][1] = wb[8 * step_of(i) + 1];
     }
-  }
-  __builtin_amdgcn_sched_barrier(0);
-  u32x4 wv[NST][VPL];
-#pragma unroll
-  for (int i = 0; i < NST; ++i) {
-    wv[i][0] = wb[8 * step_of(i)];
-    wv[i][1] = wb[8 * step_of(i) + 1];
-  }
-  __builtin_amdgcn_sched_barrier(0);
-
+    __builtin_amdgcn_sched_barrier(0);
+  };
+  int t = (int)blockIdx.x;
+  issue(t);
   __builtin_amdgcn_s_setprio(0);
 
   // 4. x -> LDS ([NT][M][K] halves); with XW a wave reads only what it wrote, and a
@@ -765,63 +779,82 @@ __global__ void __launch_bounds__(1024) gemv_fast_kernel(GemvArgs a) {
   if (!XW) __syncthreads();
 
   const MixMasks km = mix_masks();
-  floatx4 acc = {0.f, 0.f, 0.f, 0.f};
   // A row r: x row r (S = 1, rows past M repeat row M - 1) or x segment r (S = 2)
   const uint16_t* xrow = S == 1 ? lds + min(r, a.M - 1) * K : lds + (r < S ? r : 0) * KS;
+  // partial sums [2][waves][MR][16]: consecutive tiles of a workgroup use alternate halves
+  float* red = reinterpret_cast<float*>(lds + NT * plane);
+  for (int it = 0;; ++it) {
+    floatx4 acc = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-  for (int i = 0; i < NST; ++i) {
-    if (i < NST - 1 || i < cnt) {
+    for (int i = 0; i < NST; ++i) {
+      if (i < NST - 1 || i < cnt) {
 #pragma unroll
-      for (int v = 0; v < VPL; ++v) {
-        const MixScale Sc = mix_scale(v == 0 ? (sv[i] & 0xffffu) : (sv[i] >> 16));
-        const uint16_t* xr = xrow + 32 * ((s0 + i) * 8 + c * 2 + v);
-        const uint32_t wj[4] = {wv[i][v][0], wv[i][v][1], wv[i][v][2], wv[i][v][3]};
+        for (int v = 0; v < VPL; ++v) {
+          const MixScale Sc = mix_scale(v == 0 ? (sv[i] & 0xffffu) : (sv[i] >> 16));
+          const uint16_t* xr = xrow + 32 * ((s0 + i) * 8 + c * 2 + v);
+          const uint32_t wj[4] = {wv[i][v][0], wv[i][v][1], wv[i][v][2], wv[i][v][3]};
 #pragma unroll
-        for (int j = 0; j < 4; ++j) {
-          const bf16x8 bb = dequant8_mix(wj[j], Sc, km);
+          for (int j = 0; j < 4; ++j) {
+            const bf16x8 bb = dequant8_mix(wj[j], Sc, km);
 #pragma unroll
-          for (int t = 0; t < NT; ++t)
-            acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(*reinterpret_cast<const bf16x8*>(xr + t * plane + 8 * j),
-                                                          bb, acc, 0, 0, 0);
+            for (int q = 0; q < NT; ++q)
+              acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(*reinterpret_cast<const bf16x8*>(xr + q * plane + 8 * j),
+                                                            bb, acc, 0, 0, 0);
+          }
         }
       }
     }
-  }
+    // this tile's output; the next tile's loads go out before its epilogue
+    const GroupSel go = gs;
+    const int bo = bt;
+    const int tn = t + a.gstride;
+    if (PERSIST && tn < T) {
+      __builtin_amdgcn_s_setprio(3);
+      issue(tn);
+      __builtin_amdgcn_s_setprio(0);
+    }
 
-  // D: lane (r, c) holds rows m = 4c + i of column r; MR = 4 keeps c == 0 only.  With
-  // K segments, column r's sum is D[seg][r]: select it, then add the two segments of
-  // row rr (lanes rr and rr + 8, one DPP rotation apart).
-  float* red = reinterpret_cast<float*>(lds + NT * plane);  // [waves][MR][16]
-  if (S == 2) {
-    float v = seg == 0 ? acc[0] : acc[1];
-    v += lane_xor8(v);
-    if (c == 0) red[(wave * MR) * 16 + r] = v;
-  } else if (MR == 16 || c == 0) {
+    // D: lane (r, c) holds rows m = 4c + i of column r; MR = 4 keeps c == 0 only.  With
+    // K segments, column r's sum is D[seg][r]: select it, then add the two segments of
+    // row rr (lanes rr and rr + 8, one DPP rotation apart).
+    float* rb = red + (it & 1) * nwaves * MR * 16;
+    if (S == 2) {
+      float v = seg == 0 ? acc[0] : acc[1];
+      v += lane_xor8(v);
+      if (c == 0) rb[(wave * MR) * 16 + r] = v;
+    } else if (MR == 16 || c == 0) {
 #pragma unroll
-    for (int i = 0; i < 4; ++i) red[(wave * MR + (MR == 16 ? 4 * c : 0) + i) * 16 + r] = acc[i];
-  }
-  __builtin_amdgcn_s_setprio(2);
-  __syncthreads();
-  for (int t = (int)threadIdx.x; t < 16 * MR; t += (int)blockDim.x) {
-    const int m = t >> 4, ro = t & 15;
-    const int n = bt * R + ro;
-    if (pair_f) {
-      // gate row ro < 8 of the tile and its up row ro + 8
-      const int f = (bt << 3) + ro;
-      if (ro < 8 && m < a.M && f < pair_f) {
-        float g = 0.f, u = 0.f;
-        for (int w = 0; w < nwaves; ++w) {
-          g += red[(w * MR + m) * 16 + ro];
-          u += red[(w * MR + m) * 16 + ro + 8];
-        }
-        store_gelu_mul(a.y, a.y_f32, a.bf16_dots, (int64_t)m * pair_f + f, g, u);
-      }
-    } else if (m < a.M && ro < R && n < N) {
-      float v = 0.f;
-      for (int w = 0; w < nwaves; ++w) v += red[(w * MR + m) * 16 + ro];
-      if (a.y_f32) reinterpret_cast<float*>(gs.y)[(int64_t)m * N + n] = v;
-      else reinterpret_cast<uint16_t*>(gs.y)[(int64_t)m * N + n] = (uint16_t)f32_to_bf16_rne(v);
+      for (int i = 0; i < 4; ++i) rb[(wave * MR + (MR == 16 ? 4 * c : 0) + i) * 16 + r] = acc[i];
     }
+    // (the other half was last read before the previous barrier, so one barrier per tile
+    // orders both the writes above and their reads below)
+    __builtin_amdgcn_s_setprio(2);
+    __syncthreads();
+    const int N = go.N;
+    for (int e = (int)threadIdx.x; e < 16 * MR; e += 64 * nwaves) {
+      const int m = e >> 4, ro = e & 15;
+      const int n = bo * R + ro;
+      if (pair_f) {
+        // gate row ro < 8 of the tile and its up row ro + 8
+        const int f = (bo << 3) + ro;
+        if (ro < 8 && m < a.M && f < pair_f) {
+          float g = 0.f, u = 0.f;
+          for (int w = 0; w < nwaves; ++w) {
+            g += rb[(w * MR + m) * 16 + ro];
+            u += rb[(w * MR + m) * 16 + ro + 8];
+          }
+          store_gelu_mul(a.y, a.y_f32, a.bf16_dots, (int64_t)m * pair_f + f, g, u);
+        }
+      } else if (m < a.M && ro < R && n < N) {
+        float v = 0.f;
+        for (int w = 0; w < nwaves; ++w) v += rb[(w * MR + m) * 16 + ro];
+        if (a.y_f32) reinterpret_cast<float*>(go.y)[(int64_t)m * N + n] = v;
+        else reinterpret_cast<uint16_t*>(go.y)[(int64_t)m * N + n] = (uint16_t)f32_to_bf16_rne(v);
+      }
+    }
+    if (!PERSIST || tn >= T) break;
+    t = tn;
+    __builtin_amdgcn_s_setprio(0);
   }
 }
 
@@ -1715,7 +1748,7 @@ bool gemv_plan_runs(int64_t M, int64_t N, int64_t K, int nterms, int mr, bool al
   if (!nst_instanced(nst) || (nterms == 3 && nst > 5) || (mr == 16 && nst > 2)) return false;
   const int64_t nv = (int64_t)nterms * M * s * nst * 32;  // x vectors per wave
   if (nv > 64 * 8) return false;
-  if ((int64_t)nterms * M * K * 2 + nw * mr * 16 * 4 > 160 * 1024) return false;
+  if ((int64_t)nterms * M * K * 2 + nw * mr * 16 * 4 * 2 > 160 * 1024) return false;
   *out = GemvPlan{nst, (int)nw, pow2_at_least((nv + 63) / 64), true, s, (int)tiles};
   return true;
 }
@@ -1749,7 +1782,7 @@ bool gemv_plan(int64_t M, int64_t N, int64_t K, int nterms, int mr, GemvPlan* ou
     const int64_t nv = (int64_t)nterms * M * nst * 32;
     if (nv > 64 * 8) continue;
     const int waves = (int)(steps / nst);
-    if (lds_x + (int64_t)waves * mr * 16 * 4 > 160 * 1024) continue;
+    if (lds_x + (int64_t)waves * mr * 16 * 4 * 2 > 160 * 1024) continue;
     best = GemvPlan{nst, waves, pow2_at_least((nv + 63) / 64), true, 1, (int)tiles};
     have = true;
     if (tiles * waves <= GEMV_ONE_ROUND_WAVES) break;
@@ -1768,7 +1801,7 @@ bool gemv_plan(int64_t M, int64_t N, int64_t K, int nterms, int mr, GemvPlan* ou
     const int64_t nvec = (int64_t)nterms * M * K / 8;
     const int64_t per = (nvec + 64 * waves - 1) / (64 * waves);
     if (per > 8) continue;
-    if (lds_x + (int64_t)waves * mr * 16 * 4 > 160 * 1024) continue;
+    if (lds_x + (int64_t)waves * mr * 16 * 4 * 2 > 160 * 1024) continue;
     *out = GemvPlan{nst, waves, pow2_at_least(per), false, 1, (int)tiles};
     return true;
   }
@@ -1807,6 +1840,41 @@ int w4l_gemv_waves(int64_t N, int64_t K) {
   return (int)w;
 }
 
+// Workgroups of `block` threads and `lds` bytes that one CU holds at once for kernel k
+// (the occupancy query, remembered per thread for the last kernel, size and LDS asked).
+static hipError_t resident_blocks(const void* k, int block, size_t lds, int* out) {
+  struct Last {
+    const void* k;
+    int block;
+    size_t lds;
+    int n;
+  };
+  static thread_local Last last{nullptr, 0, 0, 0};
+  if (last.k == k && last.block == block && last.lds == lds) {
+    *out = last.n;
+    return hipSuccess;
+  }
+  int n = 0;
+  const hipError_t e = hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, k, block, lds);
+  if (e != hipSuccess) return e;
+  last = Last{k, block, lds, n};
+  *out = n;
+  return hipSuccess;
+}
+
+// CUs of the current device (remembered per device).
+static int device_cus() {
+  static std::atomic<int> cus[64];
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 0;
+  int n = cus[dev].load(std::memory_order_relaxed);
+  if (n == 0) {
+    if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess) return 0;
+    cus[dev].store(n, std::memory_order_relaxed);
+  }
+  return n;
+}
+
 // LDS above 64 KB per workgroup needs the kernel's attribute raised once.
 template <class Kern>
 static hipError_t allow_big_lds(Kern k, size_t lds) {
@@ -1828,9 +1896,35 @@ static hipError_t gemv_fast_one(const w4k::GemvArgs& a, dim3 grid, dim3 block, s
                         : w4k::gemv_fast_kernel<NT, NST, XPT, false, MR, XW, PL, S2>)
                  : (g32 ? w4k::gemv_fast_kernel<NT, NST, XPT, true, MR, XW, false, S2>
                         : w4k::gemv_fast_kernel<NT, NST, XPT, false, MR, XW, false, S2>);
+  // The tile loop (PLAIN, group-32 scales, M >= 3, more tiles than one round of
+  // workgroups holds): the workgroups that fit on the device at once walk the tiles, each
+  // issuing its next tile's loads before the current tile's epilogue and staging x once,
+  // instead of a second round of workgroups that starts only as first-round slots free
+  // (12B gate/up at M = 4: 19.4 -> 16.7 us).  At M = 1 and 2 it measured 1-8 % slower
+  // (the loop's code costs more than the shorter x staging and the missing second round
+  // save), and so does a one-round grid.
+  if constexpr (PL && S2 == 1) {
+    if (plain && g32 && a.M >= 3) {
+      auto kl = w4k::gemv_fast_kernel<NT, NST, XPT, true, MR, XW, true, 1, true>;
+      int per_cu = 0;
+      hipError_t e = allow_big_lds(kl, lds);
+      if (e != hipSuccess) return e;
+      e = resident_blocks(reinterpret_cast<const void*>(kl), (int)block.x, lds, &per_cu);
+      if (e != hipSuccess) return e;
+      const int64_t cap = (int64_t)per_cu * device_cus();
+      if (cap > 0 && (int64_t)grid.x > cap) {
+        w4k::GemvArgs b = a;
+        b.gstride = (int)cap;
+        hipLaunchKernelGGL(kl, dim3((unsigned)cap), block, lds, st, b);
+        return hipGetLastError();
+      }
+    }
+  }
   hipError_t e = allow_big_lds(k, lds);
   if (e != hipSuccess) return e;
-  hipLaunchKernelGGL(k, grid, block, lds, st, a);
+  w4k::GemvArgs b = a;
+  b.gstride = (int)grid.x;
+  hipLaunchKernelGGL(k, grid, block, lds, st, b);
   return hipGetLastError();
 }
 
@@ -1845,7 +1939,10 @@ static hipError_t gemv_fast_launch(const w4k::GemvArgs& a0, int nterms, int mr, 
   if (p.waves < 1 || p.waves > steps || (steps + p.waves - 1) / p.waves != p.nst) return hipErrorInvalidValue;
   a.wbase = steps / p.waves;
   a.wrem = steps % p.waves;
-  const size_t lds = (size_t)nterms * a.M * a.K * 2 + (size_t)p.waves * mr * 16 * 4;
+  a.ntiles = nblocks;
+  a.waves = p.waves;
+  // x, then two halves of partial sums (alternate tiles of a workgroup)
+  const size_t lds = (size_t)nterms * a.M * a.K * 2 + (size_t)p.waves * mr * 16 * 4 * 2;
   const dim3 grid((unsigned)nblocks), block(64 * p.waves);
 #define W4_GFS(NT_, NST_, MR_, XW_, S_)                                                           \
   switch (p.xpt) {                                                                                \

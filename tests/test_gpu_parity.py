@@ -788,9 +788,9 @@ def test_prefill_kernel_small_m(M, N, K):
 
 
 def test_linear_m4_beyond_both_gemv_plans():
-    """12B gate/up rows at M = 4 (x re-read per 16-row tile over the 16-row GEMV's
-    limit): the skinny kernel, x rows past M repeating row M - 1; every 11th row n
-    against the oracle, f32 and bf16 outputs."""
+    """12B gate/up rows at M = 4: the decode GEMV's 4-row form, whose 1 920 tiles are more
+    than one round of workgroups holds, so its tile loop (x rows past M repeating row
+    M - 1); every 11th row n against the oracle, f32 and bf16 outputs."""
     M, K, N = 4, 3840, 30720
     say(f"M=4 beyond both GEMV plans K={K} N={N}")
     _, pk, sc = o.synth_weights(N, K, 1700)
@@ -801,6 +801,24 @@ def test_linear_m4_beyond_both_gemv_plans():
     check_f32(gpu_linear(x, pk, sc, "f32")[:, rows], x, w, K, ref32)
     _, mag = o.matmul_f64(x, w)
     check_bf16(gpu_linear(x, pk, sc, "bf16")[:, rows], ref32, mag, K)
+
+
+@pytest.mark.parametrize("M,N,K", [(3, 20001, 3840), (4, 30000, 1536), (3, 30720, 3840)])
+def test_linear_decode_tile_loop(M, N, K):
+    """M = 3, 4 with more 16-row tiles than one round of workgroups holds: the decode
+    GEMV's tile loop (each workgroup walks tiles b, b + grid, ..., the next tile's loads
+    issued before the current tile's epilogue, partial sums in alternating LDS halves).
+    Every row against the oracle (f32 out), and the bf16 output equal to the f32 one
+    rounded once."""
+    say(f"decode tile loop M={M} N={N} K={K}")
+    _, pk, sc = o.synth_weights(N, K, 1800 + M)
+    x = o.synth_x(M, K, 1801 + M)
+    w = o.dequant(pk, sc)
+    ref32 = o.matmul_f32(x, w)
+    y32 = gpu_linear(x, pk, sc, "f32")
+    check_f32(y32, x, w, K, ref32)
+    yb = gpu_linear(x, pk, sc, "bf16")
+    assert np.array_equal(yb, o.f32_to_bf16(y32))
 
 
 @pytest.mark.parametrize("M,Ns,K,x_f32,out", [
