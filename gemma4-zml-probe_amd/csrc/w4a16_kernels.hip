@@ -690,10 +690,11 @@ __global__ void __launch_bounds__(1024) gemv_fast_kernel(GemvArgs a) {
   const int K = a.K;
   const int KS = (int)((unsigned)K / S);  // columns per segment
   const int plane = a.M * K;
-  // LOOP (the PLAIN form with group-32 scales): workgroup b takes tiles b, b + gstride,
-  // ... of a grid the host caps at one round; the next tile's loads go out before the
-  // current tile's epilogue and x is staged once.  Otherwise one tile per workgroup.
-  static_assert(!LOOP || (PLAIN && G32 && S == 1), "tile loop: the PLAIN group-32 form");
+  // LOOP (one weight or a gate/up pair, group-32 scales, bf16 x, the 4-row epilogue):
+  // workgroup b takes tiles b, b + gstride, ... of a grid the host caps at one round; the
+  // next tile's loads go out before the current tile's epilogue and x is staged once.
+  // Otherwise one tile per workgroup.
+  static_assert(!LOOP || (G32 && S == 1 && NT == 1 && MR == 4 && XW), "tile loop: the bf16 4-row group-32 form");
   constexpr bool PERSIST = LOOP;
   const int T = a.ntiles;  // (gridDim.x is a.gstride)
 
@@ -739,7 +740,7 @@ __global__ void __launch_bounds__(1024) gemv_fast_kernel(GemvArgs a) {
   uint32_t sv[NST];      // two bf16 scales (low half: the step's first vector)
   u32x4 wv[NST][VPL];
   auto issue = [&](int t) __attribute__((always_inline)) {
-    gs = PLAIN ? GroupSel{a.pk, a.sc, a.y, a.N, 0} : group_select(a, t);
+    gs = (PLAIN || LOOP) ? GroupSel{a.pk, a.sc, a.y, a.N, 0} : group_select(a, t);
     bt = t - gs.tile0;
     const int tile = min(bt, (gs.N + R - 1) / R - 1);
     const uint32_t* pkrow;
@@ -1896,16 +1897,17 @@ static hipError_t gemv_fast_one(const w4k::GemvArgs& a, dim3 grid, dim3 block, s
                         : w4k::gemv_fast_kernel<NT, NST, XPT, false, MR, XW, PL, S2>)
                  : (g32 ? w4k::gemv_fast_kernel<NT, NST, XPT, true, MR, XW, false, S2>
                         : w4k::gemv_fast_kernel<NT, NST, XPT, false, MR, XW, false, S2>);
-  // The tile loop (PLAIN, group-32 scales, M >= 3, more tiles than one round of
-  // workgroups holds): the workgroups that fit on the device at once walk the tiles, each
+  // The tile loop (one weight or a gate/up pair, group-32 scales, M >= 3, more tiles
+  // than one round of workgroups holds): the workgroups that fit on the device at once walk the tiles, each
   // issuing its next tile's loads before the current tile's epilogue and staging x once,
   // instead of a second round of workgroups that starts only as first-round slots free
   // (12B gate/up at M = 4: 19.4 -> 16.7 us).  At M = 1 and 2 it measured 1-8 % slower
   // (the loop's code costs more than the shorter x staging and the missing second round
   // save), and so does a one-round grid.
   if constexpr (PL && S2 == 1) {
-    if (plain && g32 && a.M >= 3) {
-      auto kl = w4k::gemv_fast_kernel<NT, NST, XPT, true, MR, XW, true, 1, true>;
+    if (a.nmat <= 1 && g32 && a.M >= 3) {
+      // (one instance for the single weight and the gate/up pair: pair_f decides)
+      auto kl = w4k::gemv_fast_kernel<NT, NST, XPT, true, MR, XW, false, 1, true>;
       int per_cu = 0;
       hipError_t e = allow_big_lds(kl, lds);
       if (e != hipSuccess) return e;
