@@ -63,6 +63,7 @@ def _call_both(x, pk, sc, M, N, K, out_f32):
     ("bf16 x, split-K route", (32, 3840, 15360), (8, 2048, 3840), False, True),
     ("bf16 x, decode GEMV", (1, 30720, 3840), (1, 4096, 3840), False, False),
     ("f32 x, planes in scratch", (16, 4096, 3840), (3, 2048, 1536), True, True),
+    ("bf16 x, decode GEMV tile loop", (4, 30720, 3840), (3, 20001, 3840), False, False),
 ])
 def test_noalloc_matches_linear(case):
     label, first, second, x_f32, out_f32 = case
