@@ -695,7 +695,6 @@ __global__ void __launch_bounds__(1024) gemv_fast_kernel(GemvArgs a) {
   // next tile's loads go out before the current tile's epilogue and x is staged once.
   // Otherwise one tile per workgroup.
   static_assert(!LOOP || (G32 && S == 1 && NT == 1 && MR == 4 && XW), "tile loop: the bf16 4-row group-32 form");
-  constexpr bool PERSIST = LOOP;
   const int T = a.ntiles;  // (gridDim.x is a.gstride)
 
   // 1. x loads, first (they need nothing but x's address; x is the same for every tile)
@@ -809,7 +808,7 @@ __global__ void __launch_bounds__(1024) gemv_fast_kernel(GemvArgs a) {
     const GroupSel go = gs;
     const int bo = bt;
     const int tn = t + a.gstride;
-    if (PERSIST && tn < T) {
+    if (LOOP && tn < T) {
       __builtin_amdgcn_s_setprio(3);
       issue(tn);
       __builtin_amdgcn_s_setprio(0);
@@ -853,7 +852,7 @@ __global__ void __launch_bounds__(1024) gemv_fast_kernel(GemvArgs a) {
         else reinterpret_cast<uint16_t*>(go.y)[(int64_t)m * N + n] = (uint16_t)f32_to_bf16_rne(v);
       }
     }
-    if (!PERSIST || tn >= T) break;
+    if (!LOOP || tn >= T) break;
     t = tn;
     __builtin_amdgcn_s_setprio(0);
   }
