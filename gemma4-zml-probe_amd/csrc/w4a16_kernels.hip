@@ -694,7 +694,7 @@ __global__ void __launch_bounds__(1024) gemv_fast_kernel(GemvArgs a) {
   // workgroup b takes tiles b, b + gstride, ... of a grid the host caps at one round; the
   // next tile's loads go out before the current tile's epilogue and x is staged once.
   // Otherwise one tile per workgroup.
-  static_assert(!LOOP || (G32 && S == 1 && NT == 1 && MR == 4 && XW), "tile loop: the bf16 4-row group-32 form");
+  static_assert(!LOOP || (G32 && S == 1 && MR == 4 && XW), "tile loop: the 4-row group-32 form");
   const int T = a.ntiles;  // (gridDim.x is a.gstride)
 
   // 1. x loads, first (they need nothing but x's address; x is the same for every tile)
@@ -1822,8 +1822,11 @@ bool w4l_gemv16_ok(int64_t M, int64_t N, int64_t K, int nterms) {
   return (N + 15) / 16 * M * K * 2 <= max_bytes;
 }
 
+// x planes in LDS up to 64 KB per workgroup; f32 x (three planes) up to the 160 KB of a CU,
+// where the alternative is the generic kernel (12B down at M = 1: 92 KB of planes)
 bool w4l_gemv_ok(int64_t M, int64_t K, int nterms) {
-  return M >= 1 && M <= 4 && (int64_t)nterms * M * K * 2 + 16 * 4 * 16 * 4 <= 65536;
+  const int64_t lim = nterms == 3 ? 160 * 1024 : 65536;
+  return M >= 1 && M <= 4 && (int64_t)nterms * M * K * 2 + 16 * 4 * 16 * 4 <= lim;
 }
 
 bool w4l_gemv_fast_ok(int64_t M, int64_t N, int64_t K, int nterms) {
@@ -1896,15 +1899,16 @@ static hipError_t gemv_fast_one(const w4k::GemvArgs& a, dim3 grid, dim3 block, s
                         : w4k::gemv_fast_kernel<NT, NST, XPT, false, MR, XW, PL, S2>)
                  : (g32 ? w4k::gemv_fast_kernel<NT, NST, XPT, true, MR, XW, false, S2>
                         : w4k::gemv_fast_kernel<NT, NST, XPT, false, MR, XW, false, S2>);
-  // The tile loop (one weight or a gate/up pair, group-32 scales, M >= 3, more tiles
-  // than one round of workgroups holds): the workgroups that fit on the device at once walk the tiles, each
-  // issuing its next tile's loads before the current tile's epilogue and staging x once,
-  // instead of a second round of workgroups that starts only as first-round slots free
-  // (12B gate/up at M = 4: 19.4 -> 16.7 us).  At M = 1 and 2 it measured 1-8 % slower
+  // The tile loop (one weight or a gate/up pair, group-32 scales, bf16 x at M >= 3 or
+  // f32 x at any M, more tiles than one round of workgroups holds): the workgroups that
+  // fit on the device at once walk the tiles, each issuing its next tile's loads before
+  // the current tile's epilogue and staging x once, instead of a second round of
+  // workgroups that starts only as first-round slots free (12B gate/up at M = 4: 19.4 ->
+  // 16.7 us; f32 x at M = 2: -7 %).  With bf16 x at M = 1 and 2 it measured 1-8 % slower
   // (the loop's code costs more than the shorter x staging and the missing second round
   // save), and so does a one-round grid.
-  if constexpr (PL && S2 == 1) {
-    if (a.nmat <= 1 && g32 && a.M >= 3) {
+  if constexpr (MR == 4 && XW && S2 == 1) {
+    if (a.nmat <= 1 && g32 && (NT == 3 || a.M >= 3)) {
       // (one instance for the single weight and the gate/up pair: pair_f decides)
       auto kl = w4k::gemv_fast_kernel<NT, NST, XPT, true, MR, XW, false, 1, true>;
       int per_cu = 0;

@@ -585,6 +585,20 @@ def test_linear_f32_activations():
         check_f32(y, x, w, K, x_f32=True)
 
 
+@pytest.mark.parametrize("M,K,N", [(1, 15360, 3840), (1, 12288, 1536), (1, 3840, 30720)])
+def test_linear_f32_activations_decode_shapes(M, K, N):
+    """f32 x at decode on the 12B down, E2B double-wide down and 12B gate/up shapes: the
+    decode GEMV with three bf16 planes of x in LDS (92 KB of planes for K = 15360, beyond
+    the 64 KB that bf16 x keeps to) and, for gate/up, the tile loop; every row against
+    the oracle."""
+    say(f"f32 activations decode M={M} K={K} N={N}")
+    _, pk, sc = o.synth_weights(N, K, 37)
+    x = np.random.default_rng(K).standard_normal((M, K), dtype=np.float32)
+    w = o.dequant(pk, sc)
+    y = gpu_linear(x, pk, sc, "f32", x_f32=True)
+    check_f32(y, x, w, K, x_f32=True)
+
+
 def test_linear_f32_activations_non_finite():
     """+-inf and NaN in f32 x follow the f32 dot (engine.zig:531-532): +-inf * w (NaN where
     w = +-0 or where infinities of both signs meet), NaN * w = NaN; the other rows are
