@@ -160,6 +160,12 @@ int w4a16_linear(const void* x, int32_t x_dtype, const int32_t* pk, const uint16
       return fail(W4A16_EWORKSPACE, "%s: f32 activations need %zu bytes of workspace, got %zu", fn,
                   need, workspace ? ws_bytes : (size_t)0);
     if ((rc = check_ptr(workspace, "workspace", fn))) return rc;
+    // the decode GEMV splits f32 x into its three bf16 planes itself (one launch, the
+    // same planes); other routes take the planes from the workspace
+    if (w4l_gemv_f32x_ok(M, N, K, group, false))
+      return hip_status(w4l_gemv(nullptr, 3, pk, sc, y, y_f32, M, N, K, group, st, nullptr,
+                                 static_cast<const float*>(x)),
+                        fn);
     uint16_t* split = static_cast<uint16_t*>(workspace);
     if ((rc = hip_status(w4l_split3(static_cast<const float*>(x), split, M * K, st), fn))) return rc;
     planes = split;
@@ -242,6 +248,10 @@ int w4a16_linear_group(const void* x, int32_t x_dtype, int32_t n, const int32_t*
       return fail(W4A16_EWORKSPACE, "%s: f32 activations need %zu bytes of workspace, got %zu", fn, need,
                   workspace ? ws_bytes : (size_t)0);
     if ((rc = check_ptr(workspace, "workspace", fn))) return rc;
+    if (w4l_group_f32x_ok(M, n, N, K, group))
+      return hip_status(w4l_gemv_group(nullptr, 3, n, pk, sc, y, N, y_f32, M, K, group, st,
+                                       static_cast<const float*>(x)),
+                        fn);
     uint16_t* split = static_cast<uint16_t*>(workspace);
     if ((rc = hip_status(w4l_split3(static_cast<const float*>(x), split, M * K, st), fn))) return rc;
     planes = split;
@@ -328,18 +338,22 @@ int w4a16_gate_up_gelu(const void* x, int32_t x_dtype, const int32_t* pk_gate, c
   const uint16_t* planes = static_cast<const uint16_t*>(x);
   int nterms = 1;
   char* ws = static_cast<char*>(workspace);
+  W4Pair pair;
+  pair.pk_up = pk_up;
+  pair.sc_up = sc_up;
+  pair.F = F;
+  pair.bf16_dots = (flags & W4A16_GATE_UP_BF16_DOTS) ? 1 : 0;
   if (x_dtype == W4A16_DTYPE_F32) {
+    if (w4l_gemv_f32x_ok(M, 16 * ((F + 7) / 8), K, group, true))
+      return hip_status(w4l_gemv(nullptr, 3, pk_gate, sc_gate, h, h_f32, M, 0, K, group, st, &pair,
+                                 static_cast<const float*>(x)),
+                        fn);
     uint16_t* split = reinterpret_cast<uint16_t*>(ws);
     if ((rc = hip_status(w4l_split3(static_cast<const float*>(x), split, M * K, st), fn))) return rc;
     planes = split;
     nterms = 3;
     ws += x_split_bytes(M, K, x_dtype);
   }
-  W4Pair pair;
-  pair.pk_up = pk_up;
-  pair.sc_up = sc_up;
-  pair.F = F;
-  pair.bf16_dots = (flags & W4A16_GATE_UP_BF16_DOTS) ? 1 : 0;
   const size_t sk = gate_up_splitk(M, F, K, x_dtype);
   if (sk && workspace != nullptr && ws_bytes >= sk)
     return hip_status(w4l_splitk(planes, pk_gate, sc_gate, h, h_f32, M, 0, K, group, st, &pair,

@@ -292,25 +292,31 @@ __global__ void __launch_bounds__(256) dequant_kernel(const uint32_t* __restrict
 // truncation), t2 the remaining <= 8 bits.  A non-finite x goes whole into t0
 // (+-inf, or the quiet NaN 0x7FC0) with t1 = t2 = +0, so the dot sees exactly
 // the f32 dot's +-inf * w and NaN * w (inf - inf in the split would make NaN).
+// The three bf16 terms of an f32 value u (bits), low 16 bits of h0, h1, h2: h0 its top
+// half (truncation), h1 the top half of the remainder, h2 the rest rounded to bf16 (RNE);
+// h0 + h1 + h2 = v exactly for finite v.  A non-finite v keeps its top half (a NaN as
+// the canonical quiet NaN 0x7fc0) and two zero terms.
+__device__ __forceinline__ void split3_terms(uint32_t u, uint32_t& h0, uint32_t& h1, uint32_t& h2) {
+  const float v = __uint_as_float(u);
+  const float t0 = __uint_as_float(u & 0xffff0000u);
+  const float r1 = v - t0;
+  const float t1 = __uint_as_float(__float_as_uint(r1) & 0xffff0000u);
+  const float r2 = r1 - t1;
+  const bool nf = (u & 0x7f800000u) == 0x7f800000u;
+  h0 = nf && (u & 0x007fffffu) ? 0x7fc0u : (u >> 16);
+  h1 = nf ? 0u : (__float_as_uint(t1) >> 16);
+  h2 = nf ? 0u : f32_to_bf16_rne(r2);
+}
+
 __global__ void __launch_bounds__(256) split3_kernel(const float* __restrict__ x,
                                                      uint16_t* __restrict__ out, int64_t n) {
   const int64_t stride = (int64_t)gridDim.x * blockDim.x;
   for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += stride) {
-    const float v = x[i];
-    const uint32_t u = __float_as_uint(v);
-    if ((u & 0x7f800000u) == 0x7f800000u) {
-      out[i] = (u & 0x007fffffu) ? (uint16_t)0x7fc0u : (uint16_t)(u >> 16);
-      out[n + i] = 0;
-      out[2 * n + i] = 0;
-      continue;
-    }
-    const float t0 = __uint_as_float(u & 0xffff0000u);
-    const float r1 = v - t0;
-    const float t1 = __uint_as_float(__float_as_uint(r1) & 0xffff0000u);
-    const float r2 = r1 - t1;
-    out[i] = (uint16_t)(u >> 16);
-    out[n + i] = (uint16_t)(__float_as_uint(t1) >> 16);
-    out[2 * n + i] = (uint16_t)f32_to_bf16_rne(r2);
+    uint32_t h0, h1, h2;
+    split3_terms(__float_as_uint(x[i]), h0, h1, h2);
+    out[i] = (uint16_t)h0;
+    out[n + i] = (uint16_t)h1;
+    out[2 * n + i] = (uint16_t)h2;
   }
 }
 
@@ -467,6 +473,8 @@ struct GemvArgs {
   // weight group (gemv_fast_kernel, TPW = 1): nmat > 1 linears that share x;
   // matrix j owns tiles [tile0[j], tile0[j + 1]) of the grid.
   int nmat;
+  // (host only) x holds f32 x [M][K], staged by the XF instances
+  int xf;
   const uint32_t* gpk[4];
   const uint16_t* gsc[4];
   void* gy[4];
@@ -668,7 +676,8 @@ __global__ void __launch_bounds__(1024) gemv_kernel(GemvArgs a) {
 // branches with late scalar loads that delay every wave's first weight load.
 // S = 2 needs NT = 1, MR = 4, XW, M = 1 and no gate/up pair (checked on the host): a
 // single weight (PLAIN) or a weight group, whose tiles are then 8-row tiles too.
-template <int NT, int NST, int XPT, bool G32, int MR, bool XW, bool PLAIN = false, int S = 1, bool LOOP = false>
+template <int NT, int NST, int XPT, bool G32, int MR, bool XW, bool PLAIN = false, int S = 1, bool LOOP = false,
+          bool XF = false>
 __global__ void __launch_bounds__(1024) gemv_fast_kernel(GemvArgs a) {
   static_assert(S == 1 || (S == 2 && NT == 1 && MR == 4 && XW), "K segments: the bf16 M = 1 form only");
   // Wave priority: high until every load of the wave is issued (a wave that has just
@@ -695,6 +704,11 @@ __global__ void __launch_bounds__(1024) gemv_fast_kernel(GemvArgs a) {
   // next tile's loads go out before the current tile's epilogue and x is staged once.
   // Otherwise one tile per workgroup.
   static_assert(!LOOP || (G32 && S == 1 && MR == 4 && XW), "tile loop: the 4-row group-32 form");
+  // XF: a.x holds f32 x [M][K] (not bf16 planes); each wave loads its share of it and writes
+  // the three bf16 terms of every value (as split3_kernel computes them) into the NT = 3
+  // planes of its LDS image, so no separate split launch precedes the GEMV.  XPT then counts
+  // 8-column vectors of f32 x per lane (two 16-byte loads each).
+  static_assert(!XF || (NT == 3 && XW && S == 1), "f32 x staging: the per-wave three-plane form");
   const int T = a.ntiles;  // (gridDim.x is a.gstride)
 
   // 1. x loads, first (they need nothing but x's address; x is the same for every tile)
@@ -708,7 +722,8 @@ __global__ void __launch_bounds__(1024) gemv_fast_kernel(GemvArgs a) {
     // clamped to the run's cnt * 32 vectors
     // (unsigned: divisions by the powers of two become shifts; with S = 2, M = NT = 1)
     constexpr unsigned per_seg = NST * 32;
-    const unsigned nv = S == 2 ? S * per_seg : NT * (unsigned)a.M * S * per_seg;
+    // (XF: the column vectors of the M rows of f32 x, each feeding all three planes)
+    const unsigned nv = S == 2 ? S * per_seg : (XF ? 1 : NT) * (unsigned)a.M * S * per_seg;
 #pragma unroll
     for (int i = 0; i < XPT; ++i) {
       const unsigned v = min((unsigned)(lane + 64 * i), nv - 1);
@@ -721,9 +736,17 @@ __global__ void __launch_bounds__(1024) gemv_fast_kernel(GemvArgs a) {
 #pragma unroll
     for (int i = 0; i < XPT; ++i) xi[i] = min((int)threadIdx.x + i * 64 * nwaves, nvec - 1);
   }
-  u32x4 xv[XPT];
+  u32x4 xv[XF ? 2 * XPT : XPT];
+  if constexpr (XF) {
 #pragma unroll
-  for (int i = 0; i < XPT; ++i) xv[i] = xsrc[xi[i]];
+    for (int i = 0; i < XPT; ++i) {
+      xv[2 * i] = xsrc[2 * xi[i]];
+      xv[2 * i + 1] = xsrc[2 * xi[i] + 1];
+    }
+  } else {
+#pragma unroll
+    for (int i = 0; i < XPT; ++i) xv[i] = xsrc[xi[i]];
+  }
   __builtin_amdgcn_sched_barrier(0);
 
   // 2. scales, then 3. weights, of this wave's NST steps of tile t (the last one clamped
@@ -774,8 +797,28 @@ __global__ void __launch_bounds__(1024) gemv_fast_kernel(GemvArgs a) {
   // 4. x -> LDS ([NT][M][K] halves); with XW a wave reads only what it wrote, and a
   // wave's LDS accesses complete in order, so no barrier is needed
   u32x4* xdst = reinterpret_cast<u32x4*>(lds);
+  if constexpr (XF) {
+    const int pv = plane >> 3;  // 16-byte vectors per plane
 #pragma unroll
-  for (int i = 0; i < XPT; ++i) xdst[xi[i]] = xv[i];
+    for (int i = 0; i < XPT; ++i) {
+      u32x4 t0, t1, t2;
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        uint32_t h0[2], h1[2], h2[2];
+#pragma unroll
+        for (int q = 0; q < 2; ++q) split3_terms(xv[2 * i + (e >> 1)][2 * (e & 1) + q], h0[q], h1[q], h2[q]);
+        t0[e] = h0[0] | (h0[1] << 16);
+        t1[e] = h1[0] | (h1[1] << 16);
+        t2[e] = h2[0] | (h2[1] << 16);
+      }
+      xdst[xi[i]] = t0;
+      xdst[pv + xi[i]] = t1;
+      xdst[2 * pv + xi[i]] = t2;
+    }
+  } else {
+#pragma unroll
+    for (int i = 0; i < XPT; ++i) xdst[xi[i]] = xv[i];
+  }
   if (!XW) __syncthreads();
 
   const MixMasks km = mix_masks();
@@ -1834,6 +1877,19 @@ bool w4l_gemv_fast_ok(int64_t M, int64_t N, int64_t K, int nterms) {
   return w4l_gemv_ok(M, K, nterms) && gemv_plan(M, N, K, nterms, 4, &p);
 }
 
+// f32 x straight into the decode GEMV (no split launch): the 4-row plan with per-wave
+// staging of three planes, group-32 scales, at most four 8-column vectors of f32 x per lane
+static bool f32x_plan_ok(const GemvPlan& p, int64_t M) {
+  return p.xw && p.s == 1 && M * p.nst * 32 <= 4 * 64;
+}
+bool w4l_gemv_f32x_ok(int64_t M, int64_t N, int64_t K, int32_t group, bool pair) {
+  GemvPlan p;
+  if (group != 32 || !w4l_gemv_ok(M, K, 3)) return false;
+  if (pair && !gemv_plan(M, N, K, 3, 4, &p)) return false;
+  if (!pair && !gemv_plan(M, N, K, 3, 4, &p, true)) return false;
+  return f32x_plan_ok(p, M);
+}
+
 int w4l_gemv_waves(int64_t N, int64_t K) {
   const int64_t steps = (K + w4k::GSTEP - 1) / w4k::GSTEP;
   int64_t w = (steps + w4k::SPW - 1) / w4k::SPW;  // every wave holds <= SPW steps
@@ -1886,9 +1942,36 @@ static hipError_t allow_big_lds(Kern k, size_t lds) {
                              160 * 1024);
 }
 
-template <int NT, int NST, int XPT, int MR, bool XW, int S = 1>
+template <int NT, int NST, int XPT, int MR, bool XW, int S = 1, bool XF = false>
 static hipError_t gemv_fast_one(const w4k::GemvArgs& a, dim3 grid, dim3 block, size_t lds, bool g32,
                                 hipStream_t st) {
+  if constexpr (XF) {
+    // f32 x staged by the GEMV itself (group-32 scales only; a weight group, a single
+    // weight or a gate/up pair, all of which read x through the same staging)
+    if (!g32) return hipErrorInvalidValue;
+    auto kf = w4k::gemv_fast_kernel<NT, NST, XPT, true, MR, XW, false, 1, false, true>;
+    if (a.nmat <= 1) {
+      auto kl = w4k::gemv_fast_kernel<NT, NST, XPT, true, MR, XW, false, 1, true, true>;
+      int per_cu = 0;
+      hipError_t e = allow_big_lds(kl, lds);
+      if (e != hipSuccess) return e;
+      e = resident_blocks(reinterpret_cast<const void*>(kl), (int)block.x, lds, &per_cu);
+      if (e != hipSuccess) return e;
+      const int64_t cap = (int64_t)per_cu * device_cus();
+      if (cap > 0 && (int64_t)grid.x > cap) {
+        w4k::GemvArgs b = a;
+        b.gstride = (int)cap;
+        hipLaunchKernelGGL(kl, dim3((unsigned)cap), block, lds, st, b);
+        return hipGetLastError();
+      }
+    }
+    hipError_t e = allow_big_lds(kf, lds);
+    if (e != hipSuccess) return e;
+    w4k::GemvArgs b = a;
+    b.gstride = (int)grid.x;
+    hipLaunchKernelGGL(kf, grid, block, lds, st, b);
+    return hipGetLastError();
+  }
   // the plain single-matrix form for bf16 x with per-wave staging and the 4-row epilogue;
   // K segments (S = 2) in that form or for a weight group (no gate/up pair), at M = 1
   constexpr bool PL = NT == 1 && MR == 4 && XW;
@@ -1993,6 +2076,27 @@ static hipError_t gemv_fast_launch(const w4k::GemvArgs& a0, int nterms, int mr, 
       default: return hipErrorInvalidValue;
     }
   }
+  if (mr == 4 && nterms == 3 && p.xw && a.xf) {
+    // f32 x staged in the kernel: XPT counts 8-column vectors of f32 x per lane
+    const int xpt = pow2_at_least(((int64_t)a.M * p.nst * 32 + 63) / 64);
+#define W4_GFX(NST_)                                                                              \
+  switch (xpt) {                                                                                  \
+    case 1: return gemv_fast_one<3, NST_, 1, 4, true, 1, true>(a, grid, block, lds, g32, st);     \
+    case 2: return gemv_fast_one<3, NST_, 2, 4, true, 1, true>(a, grid, block, lds, g32, st);     \
+    case 4: return gemv_fast_one<3, NST_, 4, 4, true, 1, true>(a, grid, block, lds, g32, st);     \
+    default: return hipErrorInvalidValue;                                                         \
+  }
+    switch (p.nst) {
+      case 1: W4_GFX(1)
+      case 2: W4_GFX(2)
+      case 3: W4_GFX(3)
+      case 4: W4_GFX(4)
+      case 5: W4_GFX(5)
+      default: return hipErrorInvalidValue;
+    }
+#undef W4_GFX
+  }
+  if (a.xf) return hipErrorInvalidValue;
   if (mr == 4 && nterms == 3 && p.xw) {
     switch (p.nst) {
       case 1: W4_GF(3, 1, 4, true)
@@ -2029,12 +2133,18 @@ static int gemv_fast_plan(int64_t M, int64_t N, int64_t K, int nterms, bool pair
 
 hipError_t w4l_gemv(const uint16_t* x_planes, int nterms, const int32_t* pk, const uint16_t* sc,
                     void* y, int y_f32, int64_t M, int64_t N, int64_t K, int32_t group,
-                    hipStream_t st, const W4Pair* pair) {
+                    hipStream_t st, const W4Pair* pair, const float* xf) {
   if (pair) N = 16 * ((pair->F + 7) / 8);
   GemvPlan p;
-  const int mr = gemv_fast_plan(M, N, K, nterms, pair != nullptr, &p);
+  const int mr = gemv_fast_plan(M, N, K, xf ? 3 : nterms, pair != nullptr, &p);
   w4k::GemvArgs a{};
   a.x = x_planes;
+  if (xf) {
+    if (!(mr == 4 && p.xw && group == 32)) return hipErrorInvalidValue;
+    a.x = reinterpret_cast<const uint16_t*>(xf);
+    a.xf = 1;
+    nterms = 3;
+  }
   a.pk = reinterpret_cast<const uint32_t*>(pk);
   a.sc = sc;
   a.y = y;
@@ -2532,16 +2642,28 @@ bool w4l_group_fused(int64_t M, int n, const int64_t* N, int64_t K, int nterms) 
   return fits && group_common_plan(M, n, N, K, nterms, &p) != 0;
 }
 
+bool w4l_group_f32x_ok(int64_t M, int n, const int64_t* N, int64_t K, int32_t group) {
+  GemvPlan p;
+  return group == 32 && w4l_group_fused(M, n, N, K, 3) && group_common_plan(M, n, N, K, 3, &p) == 4 &&
+         f32x_plan_ok(p, M);
+}
+
 hipError_t w4l_gemv_group(const uint16_t* x_planes, int nterms, int n, const int32_t* const* pk,
                           const uint16_t* const* sc, void* const* y, const int64_t* N, int y_f32, int64_t M, int64_t K,
-                          int32_t group, hipStream_t st) {
+                          int32_t group, hipStream_t st, const float* xf) {
   if (n < 1 || n > 4) return hipErrorInvalidValue;
+  if (xf) nterms = 3;
   GemvPlan p;
   const int mr = group_common_plan(M, n, N, K, nterms, &p);
   if (!mr) return hipErrorInvalidValue;
   const int R = 16 / p.s;  // W rows per tile
   w4k::GemvArgs a{};
   a.x = x_planes;
+  if (xf) {
+    if (!(mr == 4 && p.xw && group == 32)) return hipErrorInvalidValue;
+    a.x = reinterpret_cast<const uint16_t*>(xf);
+    a.xf = 1;
+  }
   a.M = (int)M;
   a.K = (int)K;
   a.group_chunks = group / 32;

@@ -38,9 +38,13 @@ int w4l_gemv_waves(int64_t N, int64_t K);
 bool w4l_gemv_fast_ok(int64_t M, int64_t N, int64_t K, int nterms);
 // With a pair, only the straight-line plans are used (hipErrorInvalidValue when
 // neither holds) and N is ignored.
+// xf: f32 x [M][K] read by the GEMV itself (its three bf16 planes staged per wave; x_planes
+// and nterms are then ignored) where w4l_gemv_f32x_ok holds (hipErrorInvalidValue otherwise).
 hipError_t w4l_gemv(const uint16_t* x_planes, int nterms, const int32_t* pk, const uint16_t* sc,
                     void* y, int y_f32, int64_t M, int64_t N, int64_t K, int32_t group,
-                    hipStream_t st, const W4Pair* pair = nullptr);
+                    hipStream_t st, const W4Pair* pair = nullptr, const float* xf = nullptr);
+// The decode GEMV takes f32 x directly (N = the pair's virtual rows 16 * ceil(F / 8) with pair).
+bool w4l_gemv_f32x_ok(int64_t M, int64_t N, int64_t K, int32_t group, bool pair);
 
 // Skinny / prefill path (M > 4, bf16 x, K % 256 == 0).
 bool w4l_skinny_ok(int64_t M, int64_t K, int nterms);
@@ -61,9 +65,11 @@ hipError_t w4l_prefill(const uint16_t* x, const int32_t* pk, const uint16_t* sc,
 // GEMV with the same plan on its own, so each y_j equals w4l_linear's bit for bit);
 // otherwise the caller runs w4l_linear per weight.
 bool w4l_group_fused(int64_t M, int n, const int64_t* N, int64_t K, int nterms);
+// xf: f32 x read by the GEMV itself (as w4l_gemv), where w4l_group_f32x_ok holds.
 hipError_t w4l_gemv_group(const uint16_t* x_planes, int nterms, int n, const int32_t* const* pk,
                           const uint16_t* const* sc, void* const* y, const int64_t* N, int y_f32, int64_t M, int64_t K,
-                          int32_t group, hipStream_t st);
+                          int32_t group, hipStream_t st, const float* xf = nullptr);
+bool w4l_group_f32x_ok(int64_t M, int n, const int64_t* N, int64_t K, int32_t group);
 
 // Fused gate/up + gelu * mul: true when one of the three kernels above takes
 // (M, F, K, nterms) in pair mode; w4l_gate_up launches it.  Otherwise the
