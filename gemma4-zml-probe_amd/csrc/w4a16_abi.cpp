@@ -109,6 +109,13 @@ size_t x_split_bytes(int64_t M, int64_t K, int32_t x_dtype) {
   if (M <= 0 || K <= 0 || x_dtype != W4A16_DTYPE_F32) return 0;
   return round_up((size_t)(3 * 2) * (size_t)M * (size_t)K, 256);
 }
+// f32 activations at M > 4: the three planes' results when the planes run as 3M rows of
+// bf16 x through the bf16 routes (optional; without it the generic three-plane kernel)
+// (then, for the 3M rows, the split-K partial sums where the bf16 route splits K)
+size_t f32_rows_bytes(int64_t M, int64_t N, int64_t K, int32_t x_dtype) {
+  if (M <= 4 || N <= 0 || K <= 0 || x_dtype != W4A16_DTYPE_F32) return 0;
+  return round_up((size_t)12 * (size_t)M * (size_t)N, 256) + round_up(w4l_splitk_bytes(3 * M, N, K, 1), 256);
+}
 // bf16 activations, 4 < M <= 64: the split-K partial sums (optional workspace;
 // without it the call takes the one-pass skinny route)
 size_t splitk_bytes(int64_t M, int64_t N, int64_t K, int32_t x_dtype) {
@@ -118,8 +125,23 @@ size_t splitk_bytes(int64_t M, int64_t N, int64_t K, int32_t x_dtype) {
 }  // namespace
 
 size_t w4a16_workspace_size(int64_t M, int64_t N, int64_t K, int32_t x_dtype) {
-  return x_split_bytes(M, K, x_dtype) + splitk_bytes(M, N, K, x_dtype);
+  return x_split_bytes(M, K, x_dtype) + f32_rows_bytes(M, N, K, x_dtype) + splitk_bytes(M, N, K, x_dtype);
 }
+
+namespace {
+// f32 x at M > 4 given the planes and f32_rows_bytes of workspace: the planes as 3M rows of
+// bf16 x through the bf16 routes into y3, then the three results added in plane order
+hipError_t f32_rows_linear(const uint16_t* planes, const int32_t* pk, const uint16_t* sc, void* y, int y_f32,
+                           int64_t M, int64_t N, int64_t K, int32_t group, float* y3, hipStream_t st) {
+  const size_t y3_bytes = round_up((size_t)12 * (size_t)M * (size_t)N, 256);
+  hipError_t e = w4l_splitk_bytes(3 * M, N, K, 1)
+                     ? w4l_splitk(planes, pk, sc, y3, 1, 3 * M, N, K, group, st, nullptr,
+                                  reinterpret_cast<float*>(reinterpret_cast<char*>(y3) + y3_bytes))
+                     : w4l_linear(planes, 1, pk, sc, y3, 1, 3 * M, N, K, group, st);
+  if (e != hipSuccess) return e;
+  return w4l_add_planes(y3, M, N, y, y_f32, st);
+}
+}  // namespace
 
 namespace {
 // argument checks shared by w4a16_linear and w4a16_linear_noalloc (no HIP call)
@@ -168,6 +190,11 @@ int w4a16_linear(const void* x, int32_t x_dtype, const int32_t* pk, const uint16
                         fn);
     uint16_t* split = static_cast<uint16_t*>(workspace);
     if ((rc = hip_status(w4l_split3(static_cast<const float*>(x), split, M * K, st), fn))) return rc;
+    const size_t rows = f32_rows_bytes(M, N, K, x_dtype);
+    if (rows && ws_bytes >= need + rows)
+      return hip_status(f32_rows_linear(split, pk, sc, y, y_f32, M, N, K, group,
+                                        reinterpret_cast<float*>(static_cast<char*>(workspace) + need), st),
+                        fn);
     planes = split;
     nterms = 3;
   } else if (workspace != nullptr && !aligned16(workspace)) {
@@ -264,10 +291,16 @@ int w4a16_linear_group(const void* x, int32_t x_dtype, int32_t n, const int32_t*
   // one launch each; with bf16 x and enough workspace a member takes the split-K
   // route as w4a16_linear would (the members run in stream order, so they share
   // the workspace one after another)
+  const size_t planes_bytes = x_split_bytes(M, K, x_dtype);
   for (int j = 0; j < n; ++j) {
     if (!N[j]) continue;
     const size_t sk = nterms == 1 && workspace != nullptr ? splitk_bytes(M, N[j], K, x_dtype) : 0;
-    if (sk && ws_bytes >= sk)
+    const size_t rows = nterms == 3 ? f32_rows_bytes(M, N[j], K, x_dtype) : 0;
+    if (rows && ws_bytes >= planes_bytes + rows)
+      rc = hip_status(f32_rows_linear(planes, pk[j], sc[j], y[j], y_f32, M, N[j], K, group,
+                                      reinterpret_cast<float*>(static_cast<char*>(workspace) + planes_bytes), st),
+                      fn);
+    else if (sk && ws_bytes >= sk)
       rc = hip_status(w4l_splitk(planes, pk[j], sc[j], y[j], y_f32, M, N[j], K, group, st, nullptr,
                                  static_cast<float*>(workspace)),
                       fn);

@@ -2456,6 +2456,10 @@ static hipError_t splitk_finalize_launch(const float* part, int kq, int64_t M, i
   return hipGetLastError();
 }
 
+hipError_t w4l_add_planes(const float* y3, int64_t M, int64_t N, void* y, int y_f32, hipStream_t st) {
+  return splitk_finalize_launch(y3, 3, M, N, y, y_f32, nullptr, st);
+}
+
 size_t w4l_splitk_bytes(int64_t M, int64_t N, int64_t K, int nterms) {
   SplitPlan p;
   if (!splitk_plan(M, N, K, nterms, &p)) return 0;

@@ -65,6 +65,10 @@ hipError_t w4l_prefill(const uint16_t* x, const int32_t* pk, const uint16_t* sc,
 // GEMV with the same plan on its own, so each y_j equals w4l_linear's bit for bit);
 // otherwise the caller runs w4l_linear per weight.
 bool w4l_group_fused(int64_t M, int n, const int64_t* N, int64_t K, int nterms);
+// y[m][n] = (y3[0][m][n] + y3[1][m][n]) + y3[2][m][n] for y3 [3][M][N] f32 (the three bf16
+// planes of f32 x run as 3M rows), f32 or bf16 (RNE) out.
+hipError_t w4l_add_planes(const float* y3, int64_t M, int64_t N, void* y, int y_f32, hipStream_t st);
+
 // xf: f32 x read by the GEMV itself (as w4l_gemv), where w4l_group_f32x_ok holds.
 hipError_t w4l_gemv_group(const uint16_t* x_planes, int nterms, int n, const int32_t* const* pk,
                           const uint16_t* const* sc, void* const* y, const int64_t* N, int y_f32, int64_t M, int64_t K,

@@ -87,7 +87,12 @@ int w4a16_dequant(const int32_t *pk, const uint16_t *sc, uint16_t *w,
 /*
  * Bytes of device workspace w4a16_linear can use for (M, N, K, x_dtype).
  * x_dtype = W4A16_DTYPE_F32: 6 * M * K bytes (rounded up to 256) to hold the
- * three bf16 terms of x, required.
+ * three bf16 terms of x, required; above M = 4 plus 12 * M * N bytes (rounded up to
+ * 256) and the bf16 split-K part for 3M rows, optional: given all of it, the three
+ * planes run as 3M rows of bf16 x through the bf16 routes and their results are
+ * added in plane order (deterministic); with only the first part, one generic kernel
+ * reads the three planes.  Both meet the same fp32 bound.  (At M <= 4 the decode
+ * GEMV splits x itself.)
  * x_dtype = W4A16_DTYPE_BF16: nothing is required.  On shapes whose one-pass
  * kernel cannot fill the GPU (K % 64 == 0, and: 64 < M <= 128, or up to 256
  * with K <= 8192, with K % 256 == 0 while the skinny kernel's grid of

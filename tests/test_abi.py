@@ -212,11 +212,13 @@ def test_workspace_size(L):
 ])
 def test_workspace_size_splitk(L, M, N, K, expect):
     """bf16 x: the optional split-K workspace (a call with less takes the
-    one-pass route); f32 x adds it to nothing (split-K is bf16-only)."""
+    one-pass route); f32 x: the planes, plus above M = 4 the optional room for the
+    three planes' results (12 * M * N bytes, rounded up to 256), and no split-K part."""
     assert splitk_bytes(M, N, K) == expect
     assert L.w4a16_workspace_size(M, N, K, w4a16.DTYPE_BF16) == expect
     planes = -(-(6 * M * K) // 256) * 256
-    assert L.w4a16_workspace_size(M, N, K, w4a16.DTYPE_F32) == planes
+    rows = -(-(12 * M * N) // 256) * 256 + splitk_bytes(3 * M, N, K) if M > 4 else 0
+    assert L.w4a16_workspace_size(M, N, K, w4a16.DTYPE_F32) == planes + rows
 
 
 _TUNING_ENV = ("W4A16_GEMV16_XBYTES", "W4A16_GEMV_NST", "W4A16_GEMV_TPW", "W4A16_GEMV16", "W4A16_GEMV_W",
