@@ -329,7 +329,10 @@ size_t gate_up_splitk(int64_t M, int64_t F, int64_t K, int32_t x_dtype) {
 }  // namespace
 
 size_t w4a16_gate_up_workspace_size(int64_t M, int64_t F, int64_t K, int32_t x_dtype) {
-  return gate_up_required(M, F, K, x_dtype) + gate_up_splitk(M, F, K, x_dtype);
+  // (f32 x above M = 4: the unfused route's optional room for the planes run as 3M rows)
+  const int nterms = x_dtype == W4A16_DTYPE_F32 ? 3 : 1;
+  const size_t rows = M > 0 && F > 0 && K > 0 && !w4l_gate_up_fused(M, F, K, nterms) ? f32_rows_bytes(M, F, K, x_dtype) : 0;
+  return gate_up_required(M, F, K, x_dtype) + gate_up_splitk(M, F, K, x_dtype) + rows;
 }
 
 int w4a16_gate_up_gelu(const void* x, int32_t x_dtype, const int32_t* pk_gate, const uint16_t* sc_gate,
@@ -395,8 +398,19 @@ int w4a16_gate_up_gelu(const void* x, int32_t x_dtype, const int32_t* pk_gate, c
   if (w4l_gate_up_fused(M, F, K, nterms))
     return hip_status(w4l_gate_up(planes, nterms, pk_gate, sc_gate, pair, h, h_f32, M, K, group, st), fn);
   // unfused route: g and u in f32 through the workspace, then the activation
+  const size_t gu = round_up((size_t)4 * (size_t)M * (size_t)F, 256);
   float* g = reinterpret_cast<float*>(ws);
-  float* u = reinterpret_cast<float*>(ws + round_up((size_t)4 * (size_t)M * (size_t)F, 256));
+  float* u = reinterpret_cast<float*>(ws + gu);
+  // f32 x above M = 4 with the optional room after g and u: each of them as w4a16_linear
+  // computes it from the planes run as 3M rows
+  char* rows_ws = ws + 2 * gu;
+  const size_t rows = nterms == 3 ? f32_rows_bytes(M, F, K, x_dtype) : 0;
+  if (rows && ws_bytes >= (size_t)(rows_ws - static_cast<char*>(workspace)) + rows) {
+    float* y3 = reinterpret_cast<float*>(rows_ws);
+    if ((rc = hip_status(f32_rows_linear(planes, pk_gate, sc_gate, g, 1, M, F, K, group, y3, st), fn))) return rc;
+    if ((rc = hip_status(f32_rows_linear(planes, pk_up, sc_up, u, 1, M, F, K, group, y3, st), fn))) return rc;
+    return hip_status(w4l_gelu_mul(g, u, h, h_f32, pair.bf16_dots, M * F, st), fn);
+  }
   if ((rc = hip_status(w4l_linear(planes, nterms, pk_gate, sc_gate, g, 1, M, F, K, group, st), fn))) return rc;
   if ((rc = hip_status(w4l_linear(planes, nterms, pk_up, sc_up, u, 1, M, F, K, group, st), fn))) return rc;
   return hip_status(w4l_gelu_mul(g, u, h, h_f32, pair.bf16_dots, M * F, st), fn);

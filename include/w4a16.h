@@ -207,7 +207,9 @@ enum {
  * limits).  Optional, added on top: bf16 x takes the split-K route of
  * w4a16_linear (same shape rules) over the 16 * ceil(F / 8) interleaved
  * gate/up rows when that row count is below 16384 (E2B: F = 6144 at M > 16),
- * with the activation applied when the parts are added.
+ * with the activation applied when the parts are added; f32 x above M = 4 (the
+ * unfused route) takes g and u each as w4a16_linear does with the optional part of
+ * w4a16_workspace_size(M, F, K, x_dtype), here the room after g and u.
  */
 size_t w4a16_gate_up_workspace_size(int64_t M, int64_t F, int64_t K, int32_t x_dtype);
 

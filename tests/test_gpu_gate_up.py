@@ -143,6 +143,7 @@ CASES = [
     (8, 40, 320, 32, False, True, False),       # unfused: K % 256 != 0 at M <= 64
     (2, 24, 96, 32, False, False, True),        # unfused, bf16 dots, h bf16
     (6, 20, 512, 32, True, True, False),        # unfused: f32 x above M = 4
+    (8, 15360, 3840, 32, True, True, False),    # 12B at M = 8, f32 x: g and u each from the planes run as 3M rows
 ]
 
 
