@@ -109,11 +109,12 @@ size_t x_split_bytes(int64_t M, int64_t K, int32_t x_dtype) {
   if (M <= 0 || K <= 0 || x_dtype != W4A16_DTYPE_F32) return 0;
   return round_up((size_t)(3 * 2) * (size_t)M * (size_t)K, 256);
 }
-// f32 activations at M > 4: the three planes' results when the planes run as 3M rows of
-// bf16 x through the bf16 routes (optional; without it the generic three-plane kernel)
+// f32 activations above M = 4 (or with planes too wide for the decode GEMV): the three
+// planes' results when the planes run as 3M rows of bf16 x through the bf16 routes
+// (optional; without it the three-plane kernels)
 // (then, for the 3M rows, the split-K partial sums where the bf16 route splits K)
 size_t f32_rows_bytes(int64_t M, int64_t N, int64_t K, int32_t x_dtype) {
-  if (M <= 4 || N <= 0 || K <= 0 || x_dtype != W4A16_DTYPE_F32) return 0;
+  if (M <= 0 || N <= 0 || K <= 0 || x_dtype != W4A16_DTYPE_F32 || !w4l_f32x_rows(M, N, K)) return 0;
   return round_up((size_t)12 * (size_t)M * (size_t)N, 256) + round_up(w4l_splitk_bytes(3 * M, N, K, 1), 256);
 }
 // bf16 activations, 4 < M <= 64: the split-K partial sums (optional workspace;
@@ -286,7 +287,14 @@ int w4a16_linear_group(const void* x, int32_t x_dtype, int32_t n, const int32_t*
   } else if (workspace != nullptr && !aligned16(workspace)) {
     return fail(W4A16_EINVAL_PTR, "%s: workspace is not 16-byte aligned", fn);
   }
-  if (w4l_group_fused(M, n, N, K, nterms))
+  // (a member that w4a16_linear would run as 3M rows of planes runs that way here too,
+  // so every y_j stays w4a16_linear's bit for bit)
+  bool rows_any = false;
+  for (int j = 0; j < n && nterms == 3; ++j) {
+    const size_t rows = f32_rows_bytes(M, N[j], K, x_dtype);
+    rows_any = rows_any || (rows && ws_bytes >= x_split_bytes(M, K, x_dtype) + rows);
+  }
+  if (!rows_any && w4l_group_fused(M, n, N, K, nterms))
     return hip_status(w4l_gemv_group(planes, nterms, n, pk, sc, y, N, y_f32, M, K, group, st), fn);
   // one launch each; with bf16 x and enough workspace a member takes the split-K
   // route as w4a16_linear would (the members run in stream order, so they share

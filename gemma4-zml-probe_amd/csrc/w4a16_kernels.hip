@@ -1877,17 +1877,31 @@ bool w4l_gemv_fast_ok(int64_t M, int64_t N, int64_t K, int nterms) {
   return w4l_gemv_ok(M, K, nterms) && gemv_plan(M, N, K, nterms, 4, &p);
 }
 
+// f32 x whose three planes take more than 64 KB of LDS at M >= 2 (one workgroup per CU)
+// over more 16-row tiles than the CUs: the planes run as 3M rows of bf16 x instead (12B
+// gate/up at M = 3, 4: 26.2 / 32.1 -> 23.1 / 23.5 us; q at M = 4, 256 tiles, stays)
+static bool f32x_wide(int64_t M, int64_t N, int64_t K) {
+  return M >= 2 && (int64_t)6 * M * K + 16 * 4 * 16 * 4 > 65536 && (N + 15) / 16 > 256;
+}
+static bool f32x_direct(int64_t M, int64_t N, int64_t K, int32_t group, bool pair);
+bool w4l_f32x_rows(int64_t M, int64_t N, int64_t K) {
+  return M > 4 || f32x_wide(M, N, K) || !f32x_direct(M, N, K, 32, false);
+}
+
 // f32 x straight into the decode GEMV (no split launch): the 4-row plan with per-wave
 // staging of three planes, group-32 scales, at most four 8-column vectors of f32 x per lane
 static bool f32x_plan_ok(const GemvPlan& p, int64_t M) {
   return p.xw && p.s == 1 && M * p.nst * 32 <= 4 * 64;
 }
-bool w4l_gemv_f32x_ok(int64_t M, int64_t N, int64_t K, int32_t group, bool pair) {
+static bool f32x_direct(int64_t M, int64_t N, int64_t K, int32_t group, bool pair) {
   GemvPlan p;
   if (group != 32 || !w4l_gemv_ok(M, K, 3)) return false;
   if (pair && !gemv_plan(M, N, K, 3, 4, &p)) return false;
   if (!pair && !gemv_plan(M, N, K, 3, 4, &p, true)) return false;
   return f32x_plan_ok(p, M);
+}
+bool w4l_gemv_f32x_ok(int64_t M, int64_t N, int64_t K, int32_t group, bool pair) {
+  return f32x_direct(M, N, K, group, pair) && !f32x_wide(M, N, K);
 }
 
 int w4l_gemv_waves(int64_t N, int64_t K) {
@@ -2648,8 +2662,10 @@ bool w4l_group_fused(int64_t M, int n, const int64_t* N, int64_t K, int nterms) 
 
 bool w4l_group_f32x_ok(int64_t M, int n, const int64_t* N, int64_t K, int32_t group) {
   GemvPlan p;
-  return group == 32 && w4l_group_fused(M, n, N, K, 3) && group_common_plan(M, n, N, K, 3, &p) == 4 &&
-         f32x_plan_ok(p, M);
+  int64_t ntot = 0;
+  for (int j = 0; j < n; ++j) ntot += N[j];
+  return group == 32 && !f32x_wide(M, ntot, K) && w4l_group_fused(M, n, N, K, 3) &&
+         group_common_plan(M, n, N, K, 3, &p) == 4 && f32x_plan_ok(p, M);
 }
 
 hipError_t w4l_gemv_group(const uint16_t* x_planes, int nterms, int n, const int32_t* const* pk,

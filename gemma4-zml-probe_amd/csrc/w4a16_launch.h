@@ -45,6 +45,9 @@ hipError_t w4l_gemv(const uint16_t* x_planes, int nterms, const int32_t* pk, con
                     hipStream_t st, const W4Pair* pair = nullptr, const float* xf = nullptr);
 // The decode GEMV takes f32 x directly (N = the pair's virtual rows 16 * ceil(F / 8) with pair).
 bool w4l_gemv_f32x_ok(int64_t M, int64_t N, int64_t K, int32_t group, bool pair);
+// f32 x better served by its planes run as 3M rows of bf16 x (M > 4, or planes beyond the
+// decode GEMV's 64 KB at M >= 2, or no decode plan)
+bool w4l_f32x_rows(int64_t M, int64_t N, int64_t K);
 
 // Skinny / prefill path (M > 4, bf16 x, K % 256 == 0).
 bool w4l_skinny_ok(int64_t M, int64_t K, int nterms);

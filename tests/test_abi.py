@@ -217,7 +217,8 @@ def test_workspace_size_splitk(L, M, N, K, expect):
     assert splitk_bytes(M, N, K) == expect
     assert L.w4a16_workspace_size(M, N, K, w4a16.DTYPE_BF16) == expect
     planes = -(-(6 * M * K) // 256) * 256
-    rows = -(-(12 * M * N) // 256) * 256 + splitk_bytes(3 * M, N, K) if M > 4 else 0
+    wide = M > 4 or (M >= 2 and 6 * M * K + 4096 > 65536) or K % 256 != 0
+    rows = -(-(12 * M * N) // 256) * 256 + splitk_bytes(3 * M, N, K) if wide else 0
     assert L.w4a16_workspace_size(M, N, K, w4a16.DTYPE_F32) == planes + rows
 
 

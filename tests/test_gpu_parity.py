@@ -841,6 +841,7 @@ def test_linear_decode_tile_loop(M, N, K):
     (1, (2048, 256, 256), 1536, False, "f32"),      # E2B q, k, v at decode (K % 512 == 0: the single linears split K in two)
     (3, (17, 0, 33, 5), 512, False, "f32"),        # ragged N, an empty member
     (2, (64, 48), 1536, True, "f32"),               # f32 x
+    (4, (4096, 2048, 2048), 3840, True, "f32"),     # f32 x at M = 4, planes beyond 64 KB: each member as 3M rows
     (20, (40, 24, 16), 256, False, "bf16"),         # above M = 16: one launch per weight
     (8, (4096, 2048, 2048), 3840, False, "f32"),     # batched decode M = 8: one launch (16-row GEMV)
     (13, (17, 0, 33, 5), 512, False, "f32"),        # M = 13, ragged N, an empty member
