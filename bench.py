@@ -39,7 +39,7 @@ LAYER_12B = [  # name, K, N
     ("gate_up", 3840, 30720), ("down", 15360, 3840),
 ]
 DOMINANT = "gate_up"
-DOMINANT_KERNEL = "w4k::gemv_fast_kernel<1, 2, 1, true, 4, true, true, 1, false>"  # the launch the M=1 plan picks for 12B gate/up
+DOMINANT_KERNEL = "w4k::gemv_fast_kernel<1, 2, 1, true, 4, true, true, 1, false, false>"  # the launch the M=1 plan picks for 12B gate/up
 TRAFFIC_FILE = os.path.join(ROOT, "profiles", "gemv_fast_12b_gateup_m1_pmc.md")
 
 
