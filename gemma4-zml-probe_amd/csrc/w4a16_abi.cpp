@@ -114,7 +114,8 @@ size_t x_split_bytes(int64_t M, int64_t K, int32_t x_dtype) {
 // (optional; without it the three-plane kernels)
 // (then, for the 3M rows, the split-K partial sums where the bf16 route splits K)
 size_t f32_rows_bytes(int64_t M, int64_t N, int64_t K, int32_t x_dtype) {
-  if (M <= 0 || N <= 0 || K <= 0 || x_dtype != W4A16_DTYPE_F32 || !w4l_f32x_rows(M, N, K)) return 0;
+  if (M <= 0 || N <= 0 || K <= 0 || x_dtype != W4A16_DTYPE_F32 || M > INT_MAX / 3 || !w4l_f32x_rows(M, N, K))
+    return 0;
   return round_up((size_t)12 * (size_t)M * (size_t)N, 256) + round_up(w4l_splitk_bytes(3 * M, N, K, 1), 256);
 }
 // bf16 activations, 4 < M <= 64: the split-K partial sums (optional workspace;
